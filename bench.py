@@ -1,0 +1,261 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused int4-KV decode attention on one MI355X.
+
+Default (the headline metric of BASELINE.json): one decode-attention layer at
+Hq=32, Hkv=16, D=256, L=32768 (BASELINE configs[2] at 32k), bf16 Q, int4 K/V
+with fp16 scale/bias.  A "step" is one call of ``sdpa_int4`` over one layer.
+Eight distinct KV sets (8 x 151 MB) are rotated so the 256 MB Infinity Cache
+cannot serve repeats; inputs are resident in HBM before timing starts.
+
+Prints ONE JSON line.  Other workloads (``--workload sweep|sliding50|ragged``)
+print their own line of the same shape.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=8, help="distinct KV sets rotated")
+    ap.add_argument("--workload", default="ctx32k",
+                    choices=["ctx32k", "sweep", "sliding50", "ragged"])
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--out", default=None, help="also append the JSON line to this file")
+    return ap.parse_args()
+
+
+def gen_cache(tq, torch, Hkv, L, D, gen, cap=None):
+    """One int4 KV set built on the GPU: RMS-normed N(0,1) K, N(0,1) V."""
+    cap = cap or L
+    kq = torch.empty((Hkv, cap, D // 8), dtype=torch.uint32, device="cuda")
+    vq = torch.empty_like(kq)
+    ks = torch.empty((Hkv, cap, D // 64), dtype=torch.float16, device="cuda")
+    kb, vs, vb = torch.empty_like(ks), torch.empty_like(ks), torch.empty_like(ks)
+    for h in range(Hkv):
+        k = torch.randn((cap, D), generator=gen, device="cuda")
+        k = k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)
+        v = torch.randn((cap, D), generator=gen, device="cuda")
+        kq[h], ks[h], kb[h] = tq.quantize(k, scale_dtype=torch.float16)
+        vq[h], vs[h], vb[h] = tq.quantize(v, scale_dtype=torch.float16)
+    return kq, ks, kb, vq, vs, vb
+
+
+def gen_q(torch, shape, gen):
+    q = torch.randn(shape, generator=gen, device="cuda")
+    q = q * torch.rsqrt(q.pow(2).mean(-1, keepdim=True) + 1e-6)
+    return q.to(torch.bfloat16)
+
+
+def time_launches(torch, fn, steps, warmup):
+    """(whole-region ms per step, mean per-launch ms) with HIP events on the
+    current stream -- the stream every launch is issued on."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i in range(steps):          # per-launch pass (kernel duration)
+        ev[i][0].record()
+        fn(i)
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in ev)
+    per_launch = sum(per) / len(per)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()                     # whole timed region, back-to-back launches
+    for i in range(steps):
+        fn(i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps, per_launch, per[len(per) // 2]
+
+
+def cpu_baseline(args, cache_host, q_host, Hq, Hkv, D, L, W, nbytes):
+    """The reference algorithm (dequantize to fp32 + fp32 softmax attention)
+    timed on this host with OpenMP -- oracle/tq_oracle.c (a port of the
+    reference's dequantize + SDPA composition, MLX is not installed)."""
+    from oracle import coracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or (os.cpu_count() or 1)
+    base = coracle.DequantSdpaBaseline(q_host, *cache_host, Hq // Hkv, 1.0, W, threads=threads)
+    base()  # warm
+    reps, t_start = 0, time.perf_counter()
+    while True:
+        base()
+        reps += 1
+        el = time.perf_counter() - t_start
+        if el >= args.cpu_seconds or reps >= 200:
+            break
+    sec = el / reps
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "us_per_layer": round(sec * 1e6, 1),
+            "sample": f"{reps} full layers (Hq={Hq} Hkv={Hkv} D={D} L={L}) of the same "
+                      f"workload, dequantize->fp32 + fp32 SDPA, oracle/tq_oracle.c OpenMP, "
+                      f"{platform.processor() or platform.machine()}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
+                          "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+        sys.exit(2)
+    import torch
+    from gemma4metal_amd import turboquant as tq
+    from oracle import oracle as O
+
+    Hq, Hkv, D = 32, 16, 256
+    gen = torch.Generator(device="cuda").manual_seed(2026)
+    res = {}
+
+    if args.workload in ("ctx32k", "sweep"):
+        lens = [args.ctx] if args.workload == "ctx32k" else [1024, 8192, 32768, 131072, 262144]
+        lines = []
+        for L in lens:
+            nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkv * L * 288)))
+            sets = [gen_cache(tq, torch, Hkv, L, D, gen) for _ in range(nsets)]
+            qs = [gen_q(torch, (Hq, D), gen) for _ in range(nsets)]
+            out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
+            nbytes = O.decode_bytes(Hq, Hkv, D, L)
+
+            def step(i):
+                s = i % nsets
+                tq.sdpa_int4(qs[s], *sets[s], Hq // Hkv, 1.0, 0, out=out)
+
+            ms_step, ms_launch, ms_med = time_launches(torch, step, args.steps, args.warmup)
+            gbs = nbytes / (ms_step * 1e-3) / 1e9
+            gbs_k = nbytes / (ms_launch * 1e-3) / 1e9
+            line = {
+                "metric": "int4-KV decode SDPA achieved HBM GB/s at 32k ctx",
+                "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+                "steps": args.steps, "warmup": args.warmup,
+                "ms_per_step": round(ms_step, 5), "us_per_layer": round(ms_step * 1e3, 2),
+                "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+                "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "dtype": "int4 K/V (fp16 scale/bias), bf16 Q, fp32 accumulate",
+                "data": "synthetic (seeded N(0,1), RMS-normed Q/K), random-init; "
+                        f"{nsets} rotated KV sets",
+                "config": {"workload": f"sdpa_int4 decode layer Hq={Hq} Hkv={Hkv} D={D} "
+                                       f"L={L} W=0 (BASELINE configs[2])",
+                           "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"},
+                "roofline": {"bound": "hbm", "achieved": round(gbs_k, 1), "peak": PEAK_GBS,
+                             "unit": "GB/s", "frac": round(gbs_k / PEAK_GBS, 4),
+                             "traffic": None, "kernel": "sdpa_int4_kernel<256,2,__half>",
+                             "bytes_per_launch": nbytes,
+                             "us_per_launch_mean": round(ms_launch * 1e3, 2),
+                             "us_per_launch_median": round(ms_med * 1e3, 2)},
+            }
+            if not args.no_cpu and L == lens[0]:
+                s0 = sets[0]
+                host = []
+                for t in s0:
+                    if t.dtype == torch.uint32:
+                        host.append(t.view(torch.int32).cpu().numpy().view("uint32"))
+                    else:
+                        host.append(t.float().cpu().numpy())
+                qh = qs[0].float().cpu().numpy()
+                line["cpu_baseline"] = cpu_baseline(args, host, qh, Hq, Hkv, D, L, 0, nbytes)
+            lines.append(line)
+            del sets
+            torch.cuda.empty_cache()
+        for line in lines:
+            emit(line, args)
+        return
+
+    if args.workload == "sliding50":
+        L, W, layers = 786, 1024, 50
+        sets = [gen_cache(tq, torch, Hkv, L, D, gen) for _ in range(layers)]
+        q = gen_q(torch, (Hq, D), gen)
+        out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
+        nbytes = O.decode_bytes(Hq, Hkv, D, L)
+
+        def one_step():
+            for s in sets:
+                tq.sdpa_int4(q, *s, Hq // Hkv, 1.0, W, out=out)
+        one_step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            one_step()
+        ms_step, ms_launch, _ = time_launches(torch, lambda i: g.replay(), args.steps, args.warmup)
+        us_layer = ms_step * 1e3 / layers
+        gbs = nbytes * layers / (ms_step * 1e-3) / 1e9
+        emit({"metric": "int4-KV decode SDPA, 50 sliding layers (HIP graph) GB/s",
+              "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+              "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+              "us_per_layer": round(us_layer, 3), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
+              "config": {"workload": "50 x sdpa_int4 Hq=32 Hkv=16 D=256 L=786 W=1024 "
+                                     "(BASELINE configs[1]), one HIP graph per step",
+                         "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"}},
+             args)
+        return
+
+    if args.workload == "ragged":
+        import numpy as np
+        B, cap = 64, 32768 + 1
+        rng = np.random.default_rng(4)
+        lens = rng.integers(512, 32768, size=B, endpoint=True).astype(np.int32)
+        wins = np.array([1024 if b % 2 == 0 else 0 for b in range(B)], np.int32)
+        cache = tq.Int4KVCache(B, Hkv, cap, D, "cuda")
+        for b in range(B):
+            c = gen_cache(tq, torch, Hkv, int(lens[b]), D, gen, cap=int(lens[b]))
+            for dst, src in zip(cache.tensors(), c):
+                dst[b, :, :int(lens[b])] = src
+        lens_d = torch.from_numpy(lens).cuda()
+        wins_d = torch.from_numpy(wins).cuda()
+        q = gen_q(torch, (B, Hq, D), gen)
+        knew = torch.randn((B, Hkv, 1, D), generator=gen, device="cuda")
+        vnew = torch.randn((B, Hkv, 1, D), generator=gen, device="cuda")
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device="cuda")
+        attended = int(sum(min(int(l) + 1, int(w)) if w else int(l) + 1
+                           for l, w in zip(lens, wins)))
+        nbytes = (Hkv * attended * 288 + B * Hq * D * 6 + 2 * B * Hkv * D * 4
+                  + 2 * B * Hkv * 144)
+
+        def step(i):
+            cache.lengths.copy_(lens_d)
+            cache.append(knew, vnew)
+            tq.sdpa_int4_ragged(q, *cache.tensors(), cache.lengths, Hq // Hkv, 1.0, 0,
+                                windows=wins_d, max_kv_len=cap, out=out)
+        ms_step, ms_launch, _ = time_launches(torch, step, args.steps, args.warmup)
+        gbs = nbytes / (ms_step * 1e-3) / 1e9
+        emit({"metric": "int4-KV ragged batched decode + append GB/s", "value": round(gbs, 1),
+              "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "ms_per_step": round(ms_step, 5), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
+              "config": {"workload": "B=64 ragged L~U[512,32768] (seed 4), W=1024 on even b, "
+                                     "append 1 fp32 token/seq then decode (BASELINE configs[3])",
+                         "global_batch": B, "seq_len": cap, "parallelism": "none (1 GPU)",
+                         "algorithmic_bytes": nbytes}}, args)
+        return
+
+
+def emit(line, args):
+    s = json.dumps(line)
+    print(s, flush=True)
+    if args.out:
+        with open(args.out, "a") as f:
+            f.write(s + "\n")
+
+
+if __name__ == "__main__":
+    main()

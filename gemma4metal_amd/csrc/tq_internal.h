@@ -1,0 +1,83 @@
+// Internal helpers shared by the HIP translation units of libturboquant_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "tq_c_api.h"
+
+namespace tq {
+
+// ---- host-side error plumbing ----------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define TQ_CHECK_ARG(cond, ...)          \
+  do {                                   \
+    if (!(cond)) {                       \
+      ::tq::set_error(__VA_ARGS__);      \
+      return TQ_ERR_INVALID;             \
+    }                                    \
+  } while (0)
+
+#define TQ_CHECK_HIP(expr)                                                     \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      ::tq::set_error("%s failed: %s", #expr, hipGetErrorString(e_));         \
+      return TQ_ERR_HIP;                                                       \
+    }                                                                          \
+  } while (0)
+
+// Launch-error check after a <<<>>> launch.
+#define TQ_CHECK_LAUNCH(name)                                                  \
+  do {                                                                         \
+    hipError_t e_ = hipGetLastError();                                         \
+    if (e_ != hipSuccess) {                                                    \
+      ::tq::set_error("launch of %s failed: %s", name, hipGetErrorString(e_)); \
+      return TQ_ERR_HIP;                                                       \
+    }                                                                          \
+  } while (0)
+
+inline bool valid_dtype(int d) { return d == TQ_F32 || d == TQ_F16 || d == TQ_BF16; }
+inline size_t dtype_size(int d) { return d == TQ_F32 ? 4 : 2; }
+
+// ---- device-side helpers ---------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Element load of a q/x tensor whose dtype is only known at run time.
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
+  if (dtype == TQ_F32) return static_cast<const float*>(p)[i];
+  if (dtype == TQ_F16) return __half2float(static_cast<const __half*>(p)[i]);
+  return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <typename SB>
+__device__ __forceinline__ float sb_to_f32(SB v);
+template <>
+__device__ __forceinline__ float sb_to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float sb_to_f32<__half>(__half v) { return __half2float(v); }
+
+template <typename SB>
+__device__ __forceinline__ SB f32_to_sb(float v);
+template <>
+__device__ __forceinline__ float f32_to_sb<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ __half f32_to_sb<__half>(float v) { return __float2half_rn(v); }
+
+// Cross-lane xor exchange inside a wave64.  Offsets < 64 only.
+__device__ __forceinline__ float shfl_xor_f(float v, int off) { return __shfl_xor(v, off, 64); }
+__device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int off) {
+  return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64));
+}
+
+// exp2 with -inf handled (v_exp_f32 returns 0 for -inf already; kept explicit).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace tq

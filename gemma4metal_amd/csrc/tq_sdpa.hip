@@ -1,0 +1,513 @@
+// Fused int4-KV decode attention (sdpa_int4) for gfx950.
+//
+// Replaces sdpa_int4_vector<D,BN> (lib/turboquant.metal:723-889) and its host
+// dispatch FusedInt4SDPA::eval_gpu (lib/turboquant.cpp:367-403).
+//
+// Work decomposition (flash-decoding):
+//   grid = (splits, kv-head x head-subgroup, batch); a workgroup of 4 wave64s
+//   owns one kv head, one contiguous chunk of keys and ALL the GQA query heads
+//   that read that kv head (G of them), so every packed K/V byte is fetched
+//   from HBM exactly once per call (the reference re-reads K/V once per query
+//   head, lib/turboquant.metal:744-745).
+//   Inside a wave, LPT = D/E consecutive lanes share one key row, each lane
+//   owning E contiguous dims (E/2 bytes of nibbles: a 16 B dwordx4 load when
+//   E = 32), so one load instruction covers 64*E/2 contiguous bytes of
+//   K (or V) rows.  The 4 waves interleave over the chunk's rows.
+//   Each lane keeps an online softmax (log2 domain) for each of its G heads;
+//   rescaling of the running output happens only when some lane's maximum
+//   grows (a wave-uniform branch), which after the first rows is rare.
+//   Epilogue: xor-exchange merge across the row groups of a wave, an LDS merge
+//   across the 4 waves, then either the final normalised output (one split)
+//   or an (O, m, l) partial in the workspace.  The last workgroup of a
+//   (sequence, kv head) -- found with one device-scope atomic counter that it
+//   resets to zero -- merges the partials with the same log-sum-exp rule, so
+//   a call is ONE kernel launch at every context length.
+//
+// Math: score_h = sum_g s_g * (q_h . n_g) + b_g * sum(q_h over g), i.e. the
+// bias term of the dequantized key (s*n + b) is folded into a per-lane
+// constant sum(q); V likewise accumulates (p*s_v)*n per element plus a per
+// group sum of p*b_v.  q is pre-multiplied by scale*log2(e) so p = exp2(.)
+// (the reference pre-scales q by scale, lib/turboquant.metal:762, and uses
+// exp; the normalised result is the same).
+#include <math.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "tq_internal.h"
+
+namespace tq {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+struct SdpaParams {
+  const void* q;
+  int q_dtype;
+  const uint32_t* kq;
+  const void* ks;
+  const void* kb;
+  const uint32_t* vq;
+  const void* vs;
+  const void* vb;
+  float* out;
+  float* ws_o;    // [B][Hq][max_splits][D]
+  float* ws_ml;   // [B][Hq][max_splits][2]
+  int* ws_cnt;    // [B][Hq]  (one counter per (sequence, kv head, head subgroup))
+  int Hq, Hkv, cap, gqa, n_sub;
+  int n;                   // single-sequence length (seq_lens == nullptr)
+  const int* seq_lens;     // device [B] or nullptr
+  const int* windows;      // device [B] or nullptr
+  int window;
+  int n_clamp;             // upper bound applied to every sequence length
+  float scale_log2;
+  int chunk;
+  int max_splits;
+};
+
+template <int D, int G>
+struct Geom {
+  static constexpr int E = G <= 2 ? 32 : (G == 4 ? 16 : 8);  // dims per lane
+  static constexpr int LPT = D / E;                          // lanes per key row
+  static constexpr int TPS = 64 / LPT;                       // rows per wave step
+  static constexpr int WPL = E / 8;                          // packed words per lane
+  static constexpr int NG = D / 64;                          // quant groups per row
+  static_assert(LPT <= 64 && 64 % LPT == 0, "bad geometry");
+};
+
+template <int WPL>
+__device__ __forceinline__ void load_words(const uint32_t* p, uint32_t w[WPL]) {
+  if constexpr (WPL == 4) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+  } else if constexpr (WPL == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    w[0] = u.x; w[1] = u.y;
+  } else {
+    w[0] = *p;
+  }
+}
+
+// The 8 nibbles of a word as floats, element order (nibble i at bits 4i).
+__device__ __forceinline__ void unpack8(uint32_t w, float n[8]) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;         // nibbles 0,2,4,6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 1,3,5,7
+  n[0] = static_cast<float>(lo & 0xFF);
+  n[1] = static_cast<float>(hi & 0xFF);
+  n[2] = static_cast<float>((lo >> 8) & 0xFF);
+  n[3] = static_cast<float>((hi >> 8) & 0xFF);
+  n[4] = static_cast<float>((lo >> 16) & 0xFF);
+  n[5] = static_cast<float>((hi >> 16) & 0xFF);
+  n[6] = static_cast<float>(lo >> 24);
+  n[7] = static_cast<float>(hi >> 24);
+}
+
+__device__ __forceinline__ float merge_factor(float m, float M) {
+  return m == -INFINITY ? 0.0f : fast_exp2(m - M);
+}
+
+template <int D, int G, typename SB>
+__global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
+  using Gm = Geom<D, G>;
+  constexpr int E = Gm::E, LPT = Gm::LPT, TPS = Gm::TPS, WPL = Gm::WPL, NG = Gm::NG;
+  constexpr int RW = D / 8;  // packed words per row
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tok = lane / LPT, j = lane % LPT;
+  const int grp = (j * E) >> 6;
+  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+
+  int n_b = p.seq_lens ? p.seq_lens[b] : p.n;
+  n_b = min(n_b, p.n_clamp);
+  const int W = p.windows ? p.windows[b] : p.window;
+  const int lo = W > 0 ? max(0, n_b - W) : 0;
+  const int L = max(n_b - lo, 0);
+  const int S = L > 0 ? (L + p.chunk - 1) / p.chunk : 1;
+  if (split >= S) return;
+  const int t_begin = lo + split * p.chunk;
+  const int t_end = min(t_begin + p.chunk, n_b);
+
+  const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
+  const uint32_t* kq = p.kq + row0 * RW + j * WPL;
+  const uint32_t* vq = p.vq + row0 * RW + j * WPL;
+  const SB* ks = static_cast<const SB*>(p.ks) + row0 * NG + grp;
+  const SB* kb = static_cast<const SB*>(p.kb) + row0 * NG + grp;
+  const SB* vs = static_cast<const SB*>(p.vs) + row0 * NG + grp;
+  const SB* vb = static_cast<const SB*>(p.vb) + row0 * NG + grp;
+
+  // q slice of every head in the group, pre-scaled by scale*log2(e).
+  float q[G][E], qsum[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const int64_t qoff = (static_cast<int64_t>(b) * p.Hq + h0 + h) * D + j * E;
+    qsum[h] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      q[h][i] = load_any(p.q, p.q_dtype, qoff + i) * p.scale_log2;
+      qsum[h] += q[h][i];
+    }
+  }
+
+  float m[G], l[G], ob[G], o[G][E];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+    ob[h] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < E; ++i) o[h][i] = 0.0f;
+  }
+
+  for (int base = t_begin + wave * TPS; base < t_end; base += kWaves * TPS) {
+    const int t = base + tok;
+    const bool valid = t < t_end;
+    const int64_t tt = valid ? t : t_end - 1;
+
+    uint32_t kw[WPL], vw[WPL];
+    load_words<WPL>(kq + tt * RW, kw);
+    load_words<WPL>(vq + tt * RW, vw);
+    const float ksc = sb_to_f32<SB>(ks[tt * NG]);
+    const float kbi = sb_to_f32<SB>(kb[tt * NG]);
+    const float vsc = sb_to_f32<SB>(vs[tt * NG]);
+    const float vbi = sb_to_f32<SB>(vb[tt * NG]);
+
+    float part[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) part[h] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) {
+      float n[8];
+      unpack8(kw[w], n);
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part[h] = fmaf(q[h][w * 8 + i], n[i], part[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) part[h] = ksc * part[h] + kbi * qsum[h];
+#pragma unroll
+    for (int off = 1; off < LPT; off <<= 1)
+#pragma unroll
+      for (int h = 0; h < G; ++h) part[h] += shfl_xor_f(part[h], off);
+
+    bool need = false;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      part[h] = valid ? part[h] : -INFINITY;
+      need |= part[h] > m[h];
+    }
+    if (__any(need)) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float mn = fmaxf(m[h], part[h]);
+        const float f = (mn == m[h]) ? 1.0f : fast_exp2(m[h] - mn);
+        l[h] *= f;
+        ob[h] *= f;
+#pragma unroll
+        for (int i = 0; i < E; ++i) o[h][i] *= f;
+        m[h] = mn;
+      }
+    }
+    float ps[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float pp = valid ? fast_exp2(part[h] - m[h]) : 0.0f;
+      l[h] += pp;
+      ob[h] = fmaf(pp, vbi, ob[h]);
+      ps[h] = pp * vsc;
+    }
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) {
+      float n[8];
+      unpack8(vw[w], n);
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[h][w * 8 + i] = fmaf(ps[h], n[i], o[h][w * 8 + i]);
+    }
+  }
+
+  // ---- epilogue: fold bias sums, merge row groups, merge waves ---------------
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < E; ++i) o[h][i] += ob[h];
+
+#pragma unroll
+  for (int off = LPT; off < 64; off <<= 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mo = shfl_xor_f(m[h], off);
+      const float lo2 = shfl_xor_f(l[h], off);
+      const float M = fmaxf(m[h], mo);
+      const float fs = merge_factor(m[h], M), fo = merge_factor(mo, M);
+      l[h] = l[h] * fs + lo2 * fo;
+#pragma unroll
+      for (int i = 0; i < E; ++i) o[h][i] = o[h][i] * fs + shfl_xor_f(o[h][i], off) * fo;
+      m[h] = M;
+    }
+  }
+
+  __shared__ float sm_o[kWaves][G][D];
+  __shared__ float sm_m[kWaves][G];
+  __shared__ float sm_l[kWaves][G];
+  if (tok == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int i = 0; i < E; ++i) sm_o[wave][h][j * E + i] = o[h][i];
+      if (j == 0) {
+        sm_m[wave][h] = m[h];
+        sm_l[wave][h] = l[h];
+      }
+    }
+  }
+  __syncthreads();
+
+  const int64_t head_base = static_cast<int64_t>(b) * p.Hq + h0;
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int h = idx / D, d = idx - (idx / D) * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
+    float O = 0.0f, Ls = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = merge_factor(sm_m[w][h], M);
+      O += sm_o[w][h][d] * f;
+      Ls += sm_l[w][h] * f;
+    }
+    if (S == 1) {
+      p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    } else {
+      const int64_t slot = (head_base + h) * p.max_splits + split;
+      p.ws_o[slot * D + d] = O;
+      if (d == 0) {
+        p.ws_ml[slot * 2] = M;
+        p.ws_ml[slot * 2 + 1] = Ls;
+      }
+    }
+  }
+  if (S == 1) return;
+
+  // ---- last workgroup of this (sequence, kv head, subgroup) merges splits ----
+  __threadfence();
+  __syncthreads();
+  __shared__ int s_last;
+  if (threadIdx.x == 0) {
+    int* cnt = p.ws_cnt + static_cast<int64_t>(b) * p.Hq + hy;
+    const int old = atomicAdd(cnt, 1);
+    s_last = (old == S - 1);
+    if (old == S - 1) atomicExch(cnt, 0);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int h = idx / D, d = idx - (idx / D) * D;
+    const int64_t slot0 = (head_base + h) * p.max_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s)
+      M = fmaxf(M, __hip_atomic_load(p.ws_ml + (slot0 + s) * 2, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT));
+    float O = 0.0f, Ls = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      const float ms = __hip_atomic_load(p.ws_ml + (slot0 + s) * 2, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+      const float ls = __hip_atomic_load(p.ws_ml + (slot0 + s) * 2 + 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+      const float f = merge_factor(ms, M);
+      O += __hip_atomic_load(p.ws_o + (slot0 + s) * D + d, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) * f;
+      Ls += ls * f;
+    }
+    p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+  }
+}
+
+// ---- host side ---------------------------------------------------------------
+
+constexpr int kTargetWgs = 1024;
+constexpr int kMinChunk = 64;
+constexpr int kChunkGranule = 32;
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : dflt;
+}
+
+int head_subgroup(int gqa) {
+  for (int g : {8, 4, 2}) if (gqa % g == 0) return g;
+  return 1;
+}
+
+// Keys per workgroup: enough workgroups to fill 256 CUs several times over,
+// never fewer than kMinChunk rows.
+int plan_chunk(int max_len, int64_t groups) {
+  const int forced = env_int("TQ_SDPA_CHUNK", 0);
+  if (forced > 0) return forced;
+  const int64_t want = (static_cast<int64_t>(max_len) * groups + kTargetWgs - 1) / kTargetWgs;
+  int64_t c = (want + kChunkGranule - 1) / kChunkGranule * kChunkGranule;
+  c = std::max<int64_t>(c, kMinChunk);
+  return static_cast<int>(std::min<int64_t>(c, 1 << 30));
+}
+
+// Upper bound of ceil(L / plan_chunk(L, groups)) over every L <= max_len
+// (plan_chunk is not monotone in L, the bound is): sizes grids and workspaces.
+int max_splits_bound(int max_len, int64_t groups) {
+  if (max_len <= 0) return 1;
+  const int forced = env_int("TQ_SDPA_CHUNK", 0);
+  if (forced > 0) return (max_len + forced - 1) / forced;
+  const int64_t by_len = (static_cast<int64_t>(max_len) + kMinChunk - 1) / kMinChunk;
+  const int64_t by_wgs = (kTargetWgs + groups - 1) / groups;
+  return static_cast<int>(std::max<int64_t>(1, std::min(by_len, by_wgs)));
+}
+
+struct WsLayout {
+  size_t cnt_off, ml_off, o_off, total;
+};
+
+WsLayout ws_layout(int batch, int Hq, int D, int max_splits) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  WsLayout w;
+  w.cnt_off = 0;
+  w.ml_off = up(sizeof(int) * static_cast<size_t>(batch) * Hq);
+  w.o_off = w.ml_off + up(sizeof(float) * 2 * static_cast<size_t>(batch) * Hq * max_splits);
+  w.total = w.o_off + up(sizeof(float) * static_cast<size_t>(batch) * Hq * max_splits * D);
+  return w;
+}
+
+template <int D, int G>
+int launch_dg(const SdpaParams& p, int sb_dtype, dim3 grid, hipStream_t s) {
+  if (sb_dtype == TQ_F16)
+    sdpa_int4_kernel<D, G, __half><<<grid, kThreads, 0, s>>>(p);
+  else
+    sdpa_int4_kernel<D, G, float><<<grid, kThreads, 0, s>>>(p);
+  TQ_CHECK_LAUNCH("sdpa_int4_kernel");
+  return TQ_OK;
+}
+
+template <int D>
+int launch_d(const SdpaParams& p, int G, int sb_dtype, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: return launch_dg<D, 1>(p, sb_dtype, grid, s);
+    case 2: return launch_dg<D, 2>(p, sb_dtype, grid, s);
+    case 4: return launch_dg<D, 4>(p, sb_dtype, grid, s);
+    default: return launch_dg<D, 8>(p, sb_dtype, grid, s);
+  }
+}
+
+int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, const void* kb,
+                const uint32_t* vq, const void* vs, const void* vb, int sb_dtype, float* out,
+                int batch, int Hq, int Hkv, int D, int cap, int n, const int32_t* seq_lens,
+                const int32_t* windows, int max_len, int gqa, float scale, int window,
+                void* workspace, size_t ws_bytes, void* stream, const char* fn) {
+  TQ_CHECK_ARG(valid_dtype(q_dtype), "%s: bad q_dtype %d", fn, q_dtype);
+  TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32, "%s: sb_dtype must be f16 or f32", fn);
+  if (D != 128 && D != 256 && D != 512) {
+    set_error("%s: head_dim must be 128, 256 or 512 (got %d)", fn, D);
+    return TQ_ERR_UNSUPPORTED;
+  }
+  TQ_CHECK_ARG(batch >= 1 && Hkv >= 1 && gqa >= 1, "%s: batch, num_kv_heads, gqa must be >= 1", fn);
+  TQ_CHECK_ARG(Hq == Hkv * gqa, "%s: num_heads (%d) != num_kv_heads (%d) * gqa_factor (%d)", fn,
+               Hq, Hkv, gqa);
+  TQ_CHECK_ARG(window >= 0, "%s: sliding_window must be >= 0", fn);
+  TQ_CHECK_ARG(max_len >= 0 && cap >= 1 && max_len <= cap,
+               "%s: need 0 <= kv_len <= kv_capacity (got %d, %d)", fn, max_len, cap);
+  TQ_CHECK_ARG(q && kq && ks && kb && vq && vs && vb && out, "%s: null tensor pointer", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(kq) % 16 == 0 && reinterpret_cast<uintptr_t>(vq) % 16 == 0,
+               "%s: k_quant / v_quant must be 16-byte aligned", fn);
+  TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
+
+  const int G = head_subgroup(gqa);
+  const int n_sub = gqa / G;
+  const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
+  int eff_len = max_len;
+  if (!seq_lens && window > 0) eff_len = std::min(max_len, window);
+  const int chunk = plan_chunk(eff_len, groups);
+  const int max_splits = max_splits_bound(eff_len, groups);
+  const WsLayout wl = ws_layout(batch, Hq, D, max_splits);
+  if (max_splits > 1) {
+    if (!workspace || ws_bytes < wl.total) {
+      set_error("%s: workspace of %zu bytes needed (got %zu)", fn, wl.total, ws_bytes);
+      return TQ_ERR_WORKSPACE;
+    }
+  }
+  TQ_CHECK_ARG(Hkv * n_sub <= 65535 && batch <= 65535, "%s: grid too large", fn);
+
+  SdpaParams p{};
+  p.q = q;
+  p.q_dtype = q_dtype;
+  p.kq = kq; p.ks = ks; p.kb = kb;
+  p.vq = vq; p.vs = vs; p.vb = vb;
+  p.out = out;
+  char* ws = static_cast<char*>(workspace);
+  p.ws_cnt = ws ? reinterpret_cast<int*>(ws + wl.cnt_off) : nullptr;
+  p.ws_ml = ws ? reinterpret_cast<float*>(ws + wl.ml_off) : nullptr;
+  p.ws_o = ws ? reinterpret_cast<float*>(ws + wl.o_off) : nullptr;
+  p.Hq = Hq; p.Hkv = Hkv; p.cap = cap; p.gqa = gqa; p.n_sub = n_sub;
+  p.n = max_len;
+  p.seq_lens = seq_lens;
+  p.windows = windows;
+  p.window = window;
+  p.n_clamp = max_len;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.chunk = chunk;
+  p.max_splits = max_splits;
+
+  dim3 grid(max_splits, Hkv * n_sub, batch);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (D) {
+    case 128: return launch_d<128>(p, G, sb_dtype, grid, s);
+    case 256: return launch_d<256>(p, G, sb_dtype, grid, s);
+    default: return launch_d<512>(p, G, sb_dtype, grid, s);
+  }
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" size_t tq_sdpa_int4_workspace_size(int batch, int num_heads, int num_kv_heads,
+                                              int head_dim, int max_kv_len) {
+  if (batch < 1 || num_kv_heads < 1 || num_heads < num_kv_heads || max_kv_len < 0) return 0;
+  const int gqa = num_heads / num_kv_heads;
+  const int G = head_subgroup(gqa);
+  const int64_t groups = static_cast<int64_t>(batch) * num_kv_heads * (gqa / G);
+  const int splits = max_splits_bound(max_kv_len, groups);
+  return ws_layout(batch, num_heads, head_dim, splits).total;
+}
+
+extern "C" int tq_sdpa_int4(const void* q, tq_dtype q_dtype, const uint32_t* k_quant,
+                            const void* k_scales, const void* k_biases, const uint32_t* v_quant,
+                            const void* v_scales, const void* v_biases, tq_dtype sb_dtype,
+                            float* out, int num_heads, int num_kv_heads, int head_dim, int kv_len,
+                            int kv_capacity, int gqa_factor, float scale, int sliding_window,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return sdpa_common(q, q_dtype, k_quant, k_scales, k_biases, v_quant, v_scales, v_biases,
+                     sb_dtype, out, 1, num_heads, num_kv_heads, head_dim, kv_capacity, kv_len,
+                     nullptr, nullptr, kv_len, gqa_factor, scale, sliding_window, workspace,
+                     workspace_bytes, stream, "tq_sdpa_int4");
+}
+
+extern "C" int tq_sdpa_int4_ragged(const void* q, tq_dtype q_dtype, const uint32_t* k_quant,
+                                   const void* k_scales, const void* k_biases,
+                                   const uint32_t* v_quant, const void* v_scales,
+                                   const void* v_biases, tq_dtype sb_dtype, float* out, int batch,
+                                   int num_heads, int num_kv_heads, int head_dim, int kv_capacity,
+                                   const int32_t* seq_lens, const int32_t* windows, int max_kv_len,
+                                   int gqa_factor, float scale, int sliding_window,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  TQ_CHECK_ARG(seq_lens != nullptr, "tq_sdpa_int4_ragged: seq_lens is NULL");
+  return sdpa_common(q, q_dtype, k_quant, k_scales, k_biases, v_quant, v_scales, v_biases,
+                     sb_dtype, out, batch, num_heads, num_kv_heads, head_dim, kv_capacity,
+                     max_kv_len, seq_lens, windows, max_kv_len, gqa_factor, scale,
+                     sliding_window, workspace, workspace_bytes, stream, "tq_sdpa_int4_ragged");
+}

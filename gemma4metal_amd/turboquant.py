@@ -1,0 +1,259 @@
+"""Python mirror of the reference's ``turboquant`` API for the int4-KV path.
+
+Function names, argument order and defaults follow ``lib/turboquant.h`` of the
+reference; tensors are torch tensors in GPU memory (torch is only the
+device-memory / stream plumbing -- every computation runs in
+``libturboquant_hip.so`` through the C ABI, see ``_lib.py``).
+
+Like the reference's ``eval_gpu`` (``lib/turboquant.cpp:372``) these wrappers
+allocate their outputs; the split-K workspace is a zero-filled per-device
+buffer grown on demand and reused (the kernels leave it zeroed).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import TQ_BF16, TQ_F16, TQ_F32, TQ_QUANT_MINMAX, TQ_QUANT_MLX, call
+
+_DT = {torch.float32: TQ_F32, torch.float16: TQ_F16, torch.bfloat16: TQ_BF16}
+_QUANT_DT = (torch.int32, torch.uint32)
+_MODES = {"mlx": TQ_QUANT_MLX, "minmax": TQ_QUANT_MINMAX}
+
+_workspaces: dict = {}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _need(cond: bool, msg: str):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_cuda(name: str, t: torch.Tensor):
+    _need(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor")
+    _need(t.is_cuda, f"{name} must be on a GPU device")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _sb_dtype(name: str, t: torch.Tensor) -> int:
+    _need(t.dtype in (torch.float16, torch.float32), f"{name} must be float16 or float32")
+    return _DT[t.dtype]
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Zero-initialised scratch of at least ``nbytes`` on ``device`` (cached)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# fused int4 decode attention
+# ---------------------------------------------------------------------------
+
+def sdpa_int4(queries: torch.Tensor,
+              k_quant: torch.Tensor, k_scales: torch.Tensor, k_biases: torch.Tensor,
+              v_quant: torch.Tensor, v_scales: torch.Tensor, v_biases: torch.Tensor,
+              gqa_factor: int, scale: float = 1.0, sliding_window: int = 0, *,
+              kv_len: Optional[int] = None, out: Optional[torch.Tensor] = None,
+              stream=None) -> torch.Tensor:
+    """``turboquant::sdpa_int4`` (reference ``lib/turboquant.h:196-207``).
+
+    queries (num_heads, head_dim) f32|f16|bf16; k_quant/v_quant
+    (num_kv_heads, N, head_dim/8) uint32 (or int32 bit patterns); scales and
+    biases (num_kv_heads, N, head_dim/64) f16|f32.  ``kv_len`` (default N, as
+    the reference's ``N = k_quant.shape(1)``, ``lib/turboquant.cpp:392``)
+    lets a preallocated cache of capacity N hold fewer valid rows.
+    Returns (num_heads, head_dim) float32.
+    """
+    for n, t in (("queries", queries), ("k_quant", k_quant), ("k_scales", k_scales),
+                 ("k_biases", k_biases), ("v_quant", v_quant), ("v_scales", v_scales),
+                 ("v_biases", v_biases)):
+        _check_cuda(n, t)
+    _need(queries.dim() == 2, "queries must be (num_heads, head_dim)")
+    _need(queries.dtype in _DT, "queries must be float32, float16 or bfloat16")
+    Hq, D = queries.shape
+    _need(k_quant.dim() == 3 and k_quant.dtype in _QUANT_DT, "k_quant must be (Hkv, N, D/8) uint32")
+    Hkv, cap, _ = k_quant.shape
+    for n, t in (("k_quant", k_quant), ("v_quant", v_quant)):
+        _need(t.shape == (Hkv, cap, D // 8) and t.dtype in _QUANT_DT, f"{n} must be ({Hkv}, {cap}, {D // 8}) uint32")
+    sbt = _sb_dtype("k_scales", k_scales)
+    for n, t in (("k_scales", k_scales), ("k_biases", k_biases), ("v_scales", v_scales),
+                 ("v_biases", v_biases)):
+        _need(t.shape == (Hkv, cap, D // 64), f"{n} must be ({Hkv}, {cap}, {D // 64})")
+        _need(_DT.get(t.dtype) == sbt, "scales and biases must share one dtype")
+    n = cap if kv_len is None else int(kv_len)
+    if out is None:
+        out = torch.empty((Hq, D), dtype=torch.float32, device=queries.device)
+    _check_cuda("out", out)
+    _need(out.shape == (Hq, D) and out.dtype == torch.float32, "out must be (Hq, D) float32")
+    nbytes = _lib.load().tq_sdpa_int4_workspace_size(1, Hq, Hkv, D, n)
+    ws = workspace(nbytes, queries.device)
+    call("tq_sdpa_int4", _ptr(queries), _DT[queries.dtype], _ptr(k_quant), _ptr(k_scales),
+         _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out),
+         Hq, Hkv, D, n, cap, int(gqa_factor), float(scale), int(sliding_window), _ptr(ws),
+         ws.numel(), _stream(stream))
+    return out
+
+
+def sdpa_int4_ragged(queries: torch.Tensor,
+                     k_quant: torch.Tensor, k_scales: torch.Tensor, k_biases: torch.Tensor,
+                     v_quant: torch.Tensor, v_scales: torch.Tensor, v_biases: torch.Tensor,
+                     seq_lens: torch.Tensor, gqa_factor: int, scale: float = 1.0,
+                     sliding_window: int = 0, *, windows: Optional[torch.Tensor] = None,
+                     max_kv_len: Optional[int] = None, out: Optional[torch.Tensor] = None,
+                     stream=None) -> torch.Tensor:
+    """Batched ragged decode.  queries (B, Hq, D); caches (B, Hkv, cap, .);
+    ``seq_lens`` / ``windows`` int32 device tensors of length B.
+    ``max_kv_len`` must bound every length (defaults to the capacity)."""
+    _check_cuda("queries", queries)
+    _need(queries.dim() == 3 and queries.dtype in _DT, "queries must be (B, Hq, D)")
+    B, Hq, D = queries.shape
+    _check_cuda("k_quant", k_quant)
+    _need(k_quant.dim() == 4 and k_quant.shape[0] == B and k_quant.dtype in _QUANT_DT,
+          "k_quant must be (B, Hkv, cap, D/8) uint32")
+    _, Hkv, cap, _ = k_quant.shape
+    for n, t in (("k_quant", k_quant), ("v_quant", v_quant)):
+        _check_cuda(n, t)
+        _need(t.shape == (B, Hkv, cap, D // 8), f"{n} must be ({B}, {Hkv}, {cap}, {D // 8})")
+    sbt = _sb_dtype("k_scales", k_scales)
+    for n, t in (("k_scales", k_scales), ("k_biases", k_biases), ("v_scales", v_scales),
+                 ("v_biases", v_biases)):
+        _check_cuda(n, t)
+        _need(t.shape == (B, Hkv, cap, D // 64) and _DT.get(t.dtype) == sbt,
+              f"{n} must be ({B}, {Hkv}, {cap}, {D // 64}) of one scale dtype")
+    _check_cuda("seq_lens", seq_lens)
+    _need(seq_lens.dtype == torch.int32 and seq_lens.numel() == B, "seq_lens must be int32 [B]")
+    if windows is not None:
+        _check_cuda("windows", windows)
+        _need(windows.dtype == torch.int32 and windows.numel() == B, "windows must be int32 [B]")
+    mx = cap if max_kv_len is None else int(max_kv_len)
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+    nbytes = _lib.load().tq_sdpa_int4_workspace_size(B, Hq, Hkv, D, mx)
+    ws = workspace(nbytes, queries.device)
+    call("tq_sdpa_int4_ragged", _ptr(queries), _DT[queries.dtype], _ptr(k_quant),
+         _ptr(k_scales), _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt,
+         _ptr(out), B, Hq, Hkv, D, cap, _ptr(seq_lens), _ptr(windows), mx, int(gqa_factor),
+         float(scale), int(sliding_window), _ptr(ws), ws.numel(), _stream(stream))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# quantize / dequantize / append
+# ---------------------------------------------------------------------------
+
+def quantize(x: torch.Tensor, group_size: int = 64, bits: int = 4, *,
+             scale_dtype: Optional[torch.dtype] = None, mode: str = "mlx", stream=None):
+    """MLX ``quantize(x, group_size, bits)`` over the last axis (the call at
+    reference ``engine/gemma4_multilayer.cpp:228``).  Returns
+    ``(w_q uint32 [..., D/8], scales [..., D/64], biases [..., D/64])``;
+    scales/biases are in ``scale_dtype`` (default: x's dtype if f16/f32)."""
+    _check_cuda("x", x)
+    _need(x.dtype in _DT, "x must be float32, float16 or bfloat16")
+    D = x.shape[-1]
+    if scale_dtype is None:
+        scale_dtype = x.dtype if x.dtype in (torch.float16, torch.float32) else torch.float16
+    _need(scale_dtype in (torch.float16, torch.float32), "scale_dtype must be float16 or float32")
+    lead = tuple(x.shape[:-1])
+    rows = x.numel() // D if D else 0
+    wq = torch.empty(lead + (D // 8,), dtype=torch.uint32, device=x.device)
+    s = torch.empty(lead + (D // 64,), dtype=scale_dtype, device=x.device)
+    b = torch.empty_like(s)
+    call("tq_quantize_int4", _ptr(x), _DT[x.dtype], rows, D, group_size, bits, _MODES[mode],
+         _ptr(wq), _ptr(s), _ptr(b), _DT[scale_dtype], _stream(stream))
+    return wq, s, b
+
+
+def dequantize(w_q: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               group_size: int = 64, bits: int = 4, *, stream=None) -> torch.Tensor:
+    """MLX ``dequantize`` (reference ``engine/gemma4_multilayer.cpp:307``):
+    ``scale * nibble + bias`` as float32, shape ``[..., 8 * w_q.shape[-1]]``."""
+    for n, t in (("w_q", w_q), ("scales", scales), ("biases", biases)):
+        _check_cuda(n, t)
+    _need(group_size == 64 and bits == 4, "only group_size=64, bits=4")
+    D = w_q.shape[-1] * 8
+    sbt = _sb_dtype("scales", scales)
+    out = torch.empty(tuple(w_q.shape[:-1]) + (D,), dtype=torch.float32, device=w_q.device)
+    rows = w_q.numel() // w_q.shape[-1] if w_q.numel() else 0
+    call("tq_dequantize_int4", _ptr(w_q), _ptr(scales), _ptr(biases), sbt, rows, D, _ptr(out),
+         _stream(stream))
+    return out
+
+
+class Int4KVCache:
+    """Preallocated int4 KV cache [B, Hkv, capacity, .] with per-sequence
+    lengths on the device: the in-place replacement for the reference's
+    per-token ``concatenate`` (``engine/gemma4_multilayer.cpp:230-240``)."""
+
+    def __init__(self, batch: int, num_kv_heads: int, capacity: int, head_dim: int,
+                 device, scale_dtype: torch.dtype = torch.float16):
+        kw = dict(device=device)
+        self.B, self.Hkv, self.cap, self.D = batch, num_kv_heads, capacity, head_dim
+        self.kq = torch.zeros((batch, num_kv_heads, capacity, head_dim // 8), dtype=torch.uint32, **kw)
+        self.vq = torch.zeros_like(self.kq)
+        self.ks = torch.zeros((batch, num_kv_heads, capacity, head_dim // 64), dtype=scale_dtype, **kw)
+        self.kb = torch.zeros_like(self.ks)
+        self.vs = torch.zeros_like(self.ks)
+        self.vb = torch.zeros_like(self.ks)
+        self.lengths = torch.zeros(batch, dtype=torch.int32, **kw)
+
+    def tensors(self):
+        return self.kq, self.ks, self.kb, self.vq, self.vs, self.vb
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor, *, mode: str = "mlx",
+               advance: bool = True, stream=None):
+        """Quantize (B, Hkv, T, D) new rows into rows [len_b, len_b+T)."""
+        kv_append_int4(k_new, v_new, *self.tensors(), self.lengths, mode=mode, stream=stream)
+        if advance:
+            self.lengths += k_new.shape[2]
+
+    def attend(self, queries: torch.Tensor, gqa_factor: int, scale: float = 1.0,
+               sliding_window: int = 0, windows: Optional[torch.Tensor] = None,
+               max_kv_len: Optional[int] = None, stream=None) -> torch.Tensor:
+        return sdpa_int4_ragged(queries, *self.tensors(), self.lengths, gqa_factor, scale,
+                                sliding_window, windows=windows, max_kv_len=max_kv_len,
+                                stream=stream)
+
+
+def kv_append_int4(k_new: torch.Tensor, v_new: torch.Tensor,
+                   k_quant: torch.Tensor, k_scales: torch.Tensor, k_biases: torch.Tensor,
+                   v_quant: torch.Tensor, v_scales: torch.Tensor, v_biases: torch.Tensor,
+                   positions: torch.Tensor, *, mode: str = "mlx", stream=None) -> None:
+    """Quantize k_new / v_new (B, Hkv, T, D) and write them at rows
+    positions[b] .. positions[b]+T-1 of the (B, Hkv, cap, .) caches."""
+    for n, t in (("k_new", k_new), ("v_new", v_new), ("k_quant", k_quant),
+                 ("k_scales", k_scales), ("k_biases", k_biases), ("v_quant", v_quant),
+                 ("v_scales", v_scales), ("v_biases", v_biases), ("positions", positions)):
+        _check_cuda(n, t)
+    _need(k_new.dim() == 4 and k_new.shape == v_new.shape and k_new.dtype == v_new.dtype,
+          "k_new / v_new must both be (B, Hkv, T, D) of one dtype")
+    _need(k_new.dtype in _DT, "k_new must be float32, float16 or bfloat16")
+    B, Hkv, T, D = k_new.shape
+    _need(k_quant.dim() == 4 and k_quant.shape[:2] == (B, Hkv) and k_quant.shape[3] == D // 8,
+          "cache must be (B, Hkv, cap, D/8)")
+    cap = k_quant.shape[2]
+    sbt = _sb_dtype("k_scales", k_scales)
+    _need(positions.dtype == torch.int32 and positions.numel() == B, "positions must be int32 [B]")
+    call("tq_kv_append_int4", _ptr(k_new), _ptr(v_new), _DT[k_new.dtype], _ptr(k_quant),
+         _ptr(k_scales), _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, B,
+         Hkv, D, cap, _ptr(positions), T, _MODES[mode], _stream(stream))
+
+
+def version() -> int:
+    return _lib.load().tq_version()

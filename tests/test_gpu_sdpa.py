@@ -1,0 +1,128 @@
+"""GPU parity: fused int4 decode attention vs the oracle (2e-3 abs / 1e-3 rel)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.gpu_util import assert_close, dev, host, queries
+
+pytestmark = pytest.mark.gpu
+
+
+def host_cache(rng, Hkv, cap, D, sb="f16"):
+    k = O.rms_norm(rng.standard_normal((Hkv, cap, D)).astype(np.float32))
+    v = rng.standard_normal((Hkv, cap, D)).astype(np.float32)
+    return O.quantize_int4(k, sb) + O.quantize_int4(v, sb)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,L,W,qdt,sb,scale", [
+    (2, 1, 128, 33, 0, "f32", "f32", 1.0),        # BASELINE config 1 (tiny)
+    (2, 1, 128, 33, 0, "f32", "f16", 1.0),
+    (16, 16, 256, 10, 0, "f32", "f32", 1.0),      # reference test shape
+    (32, 16, 256, 786, 1024, "bf16", "f16", 1.0), # BASELINE config 2 layer
+    (32, 16, 256, 1500, 1024, "bf16", "f16", 1.0),  # window active
+    (32, 4, 512, 300, 0, "bf16", "f16", 1.0),     # Gemma global layer (GQA 8, D 512)
+    (8, 1, 512, 129, 0, "f16", "f32", 0.0625),
+    (12, 4, 128, 1000, 0, "bf16", "f16", 1.0),    # GQA 3 -> head subgroups of 1
+    (24, 4, 256, 640, 100, "bf16", "f16", 1.0),   # GQA 6 -> subgroups of 2
+    (16, 4, 128, 5000, 0, "bf16", "f16", 1.0),    # GQA 4
+    (4, 4, 256, 1, 0, "bf16", "f16", 1.0),        # single key
+    (32, 16, 256, 8192, 0, "bf16", "f16", 1.0),   # many splits
+])
+def test_sdpa_matches_oracle(gpu, Hq, Hkv, D, L, W, qdt, sb, scale):
+    rng = np.random.default_rng(Hq * 7919 + L * 31 + D)
+    qd, qv = queries(rng, (Hq, D), qdt)
+    c = host_cache(rng, Hkv, L, D, sb)
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv, scale, W)
+    ref = O.sdpa_int4(qv, *c, Hq // Hkv, scale, W)
+    assert_close(host(out), ref, f"Hq{Hq} Hkv{Hkv} D{D} L{L} W{W}")
+
+
+def test_sdpa_prefix_of_capacity_and_repeat_calls(gpu):
+    rng = np.random.default_rng(3)
+    Hq, Hkv, D, cap = 32, 16, 256, 3000
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    c = host_cache(rng, Hkv, cap, D)
+    cd = [dev(a) for a in c]
+    for n in (2999, 1, 64, 65, 1234, 3000):
+        out = gpu.sdpa_int4(qd, *cd, 2, 1.0, 0, kv_len=n)
+        assert_close(host(out), O.sdpa_int4(qv, *c, 2, 1.0, 0, kv_len=n), f"kv_len {n}")
+    # repeated identical calls are bit-identical (workspace counters reset)
+    a = host(gpu.sdpa_int4(qd, *cd, 2, kv_len=2500))
+    b = host(gpu.sdpa_int4(qd, *cd, 2, kv_len=2500))
+    assert np.array_equal(a, b)
+
+
+def test_sdpa_empty_keys_zero(gpu):
+    rng = np.random.default_rng(4)
+    qd, qv = queries(rng, (4, 128), "bf16")
+    c = host_cache(rng, 2, 8, 128)
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], 2, kv_len=0)
+    assert np.all(host(out) == 0)
+
+
+def test_sdpa_full_context_split_k(gpu):
+    """BASELINE config 3 at its largest size (L=262144): cache built on the GPU
+    by the (separately bit-exact) quantize kernel, checked against the C oracle
+    on the heads of two kv heads."""
+    from oracle import coracle
+    Hq, Hkv, D, L = 32, 16, 256, 262144
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    kq = torch.empty((Hkv, L, D // 8), dtype=torch.uint32, device="cuda")
+    vq = torch.empty_like(kq)
+    ks = torch.empty((Hkv, L, D // 64), dtype=torch.float16, device="cuda")
+    kb, vs, vb = torch.empty_like(ks), torch.empty_like(ks), torch.empty_like(ks)
+    for h in range(Hkv):
+        k = torch.randn((L, D), generator=g, device="cuda")
+        k = k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)
+        v = torch.randn((L, D), generator=g, device="cuda")
+        kq[h], ks[h], kb[h] = gpu.quantize(k, scale_dtype=torch.float16)
+        vq[h], vs[h], vb[h] = gpu.quantize(v, scale_dtype=torch.float16)
+    rng = np.random.default_rng(77)
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    out = host(gpu.sdpa_int4(qd, kq, ks, kb, vq, vs, vb, 2))
+    for kvh in (0, 15):
+        sl = slice(kvh, kvh + 1)
+        c = [host(t[sl]) for t in (kq, ks, kb, vq, vs, vb)]
+        ref = coracle.sdpa_int4_f64(qv[2 * kvh:2 * kvh + 2], *c, 2)
+        assert_close(out[2 * kvh:2 * kvh + 2], ref, f"L=262144 kv head {kvh}")
+
+
+@pytest.mark.parametrize("sb", ["f16", "f32"])
+def test_ragged_batch_matches_oracle(gpu, sb):
+    rng = np.random.default_rng(21)
+    B, Hq, Hkv, D, cap = 9, 32, 16, 256, 2100
+    lens = np.array([2100, 0, 1, 513, 1024, 1025, 64, 2000, 777], np.int32)
+    wins = np.array([1024, 0, 1024, 0, 1024, 1024, 0, 5, 1024], np.int32)
+    qd, qv = queries(rng, (B, Hq, D), "bf16")
+    k = O.rms_norm(rng.standard_normal((B, Hkv, cap, D)).astype(np.float32))
+    v = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    c = O.quantize_int4(k, sb) + O.quantize_int4(v, sb)
+    out = gpu.sdpa_int4_ragged(qd, *[dev(a) for a in c], dev(lens), 2, windows=dev(wins))
+    ref = O.sdpa_int4_ragged(qv, *c, lens, wins, 2)
+    assert_close(host(out), ref, "ragged")
+
+
+def test_append_then_attend_round_trip(gpu):
+    """Config-4 step at reduced size: quantize+append one fp32 token per
+    sequence, then ragged decode over the grown caches."""
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv, D, cap = 6, 32, 16, 256, 1200
+    lens0 = np.array([1000, 10, 1100, 512, 700, 1199], np.int32)
+    wins = np.array([1024, 0] * 3, np.int32)
+    cache = gpu.Int4KVCache(B, Hkv, cap, D, "cuda")
+    k0 = O.rms_norm(rng.standard_normal((B, Hkv, cap, D)).astype(np.float32))
+    v0 = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    hc = O.quantize_int4(k0) + O.quantize_int4(v0)
+    for t, a in zip(cache.tensors(), hc):
+        t.copy_(dev(a))
+    cache.lengths.copy_(dev(lens0))
+    kn = O.rms_norm(rng.standard_normal((B, Hkv, 1, D)).astype(np.float32))
+    vn = rng.standard_normal((B, Hkv, 1, D)).astype(np.float32)
+    cache.append(dev(kn), dev(vn))
+    qd, qv = queries(rng, (B, Hq, D), "bf16")
+    out = cache.attend(qd, 2, windows=dev(wins))
+    ref_cache = dict(zip(["kq", "ks", "kb", "vq", "vs", "vb"], [a.copy() for a in hc]))
+    O.kv_append_int4(ref_cache, kn, vn, lens0)
+    ref = O.sdpa_int4_ragged(qv, *ref_cache.values(), lens0 + 1, wins, 2)
+    assert_close(host(out), ref, "append+attend")
