@@ -77,6 +77,27 @@ __device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int off) {
   return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64));
 }
 
+// Butterfly sum over aligned groups of N consecutive lanes (N <= 64), every
+// lane of the group receiving the total.  Within a row of 16 lanes this uses
+// DPP (quad_perm xor-1 / xor-2, half-row mirror, row mirror), which is exact
+// for a butterfly because after the first two steps all lanes of a quad hold
+// the same value; beyond 16 lanes it falls back to ds_bpermute.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "N");
+  if constexpr (N >= 2)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  if constexpr (N >= 4)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  if constexpr (N >= 8)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  if constexpr (N >= 16)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // exp2 with -inf handled (v_exp_f32 returns 0 for -inf already; kept explicit).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -33,38 +33,14 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <string>
 
-#include "tq_internal.h"
+#include "tq_sdpa_common.h"
 
 namespace tq {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-
-struct SdpaParams {
-  const void* q;
-  int q_dtype;
-  const uint32_t* kq;
-  const void* ks;
-  const void* kb;
-  const uint32_t* vq;
-  const void* vs;
-  const void* vb;
-  float* out;
-  float* ws_o;    // [B][Hq][max_splits][D]
-  float* ws_ml;   // [B][Hq][max_splits][2]
-  int* ws_cnt;    // [B][Hq]  (one counter per (sequence, kv head, head subgroup))
-  int Hq, Hkv, cap, gqa, n_sub;
-  int n;                   // single-sequence length (seq_lens == nullptr)
-  const int* seq_lens;     // device [B] or nullptr
-  const int* windows;      // device [B] or nullptr
-  int window;
-  int n_clamp;             // upper bound applied to every sequence length
-  float scale_log2;
-  int chunk;
-  int max_splits;
-};
+constexpr int kPrefetch = 4;  // row steps in flight per wave
 
 template <int D, int G>
 struct Geom {
@@ -89,6 +65,24 @@ __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t w[WPL]) {
   }
 }
 
+// One key/value row slice of one lane: packed K and V words plus the
+// scale/bias of the lane's quant group.  Pointers are pre-offset to the lane's
+// words / group; t is the row index.
+template <int D, int WPL, typename SB>
+struct RowBuf {
+  uint32_t kw[WPL], vw[WPL];
+  SB ks, kb, vs, vb;
+  __device__ __forceinline__ void load(const uint32_t* kq, const uint32_t* vq, const SB* ksp,
+                                       const SB* kbp, const SB* vsp, const SB* vbp, int64_t t) {
+    load_words<WPL>(kq + t * (D / 8), kw);
+    load_words<WPL>(vq + t * (D / 8), vw);
+    ks = ksp[t * (D / 64)];
+    kb = kbp[t * (D / 64)];
+    vs = vsp[t * (D / 64)];
+    vb = vbp[t * (D / 64)];
+  }
+};
+
 // The 8 nibbles of a word as floats, element order (nibble i at bits 4i).
 __device__ __forceinline__ void unpack8(uint32_t w, float n[8]) {
   const uint32_t lo = w & 0x0F0F0F0Fu;         // nibbles 0,2,4,6 in bytes 0..3
@@ -101,10 +95,6 @@ __device__ __forceinline__ void unpack8(uint32_t w, float n[8]) {
   n[5] = static_cast<float>((hi >> 16) & 0xFF);
   n[6] = static_cast<float>(lo >> 24);
   n[7] = static_cast<float>(hi >> 24);
-}
-
-__device__ __forceinline__ float merge_factor(float m, float M) {
-  return m == -INFINITY ? 0.0f : fast_exp2(m - M);
 }
 
 template <int D, int G, typename SB>
@@ -120,15 +110,9 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
   const int h0 = kvh * p.gqa + sub * G;
 
-  int n_b = p.seq_lens ? p.seq_lens[b] : p.n;
-  n_b = min(n_b, p.n_clamp);
-  const int W = p.windows ? p.windows[b] : p.window;
-  const int lo = W > 0 ? max(0, n_b - W) : 0;
-  const int L = max(n_b - lo, 0);
-  const int S = L > 0 ? (L + p.chunk - 1) / p.chunk : 1;
-  if (split >= S) return;
-  const int t_begin = lo + split * p.chunk;
-  const int t_end = min(t_begin + p.chunk, n_b);
+  const SplitRange rg = split_range(p, b, split);
+  if (split >= rg.S) return;
+  const int S = rg.S, t_begin = rg.t_begin, t_end = rg.t_end;
 
   const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
   const uint32_t* kq = p.kq + row0 * RW + j * WPL;
@@ -138,15 +122,18 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
   const SB* vs = static_cast<const SB*>(p.vs) + row0 * NG + grp;
   const SB* vb = static_cast<const SB*>(p.vb) + row0 * NG + grp;
 
-  // q slice of every head in the group, pre-scaled by scale*log2(e).
+  // q slice of every head in the group, pre-scaled by scale*log2(e).  The
+  // dtype branch is uniform and taken once; each lane reads E contiguous
+  // elements with 16 B loads.
   float q[G][E], qsum[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const int64_t qoff = (static_cast<int64_t>(b) * p.Hq + h0 + h) * D + j * E;
+    load_q_slice<E>(p.q, p.q_dtype, qoff, q[h]);
     qsum[h] = 0.0f;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      q[h][i] = load_any(p.q, p.q_dtype, qoff + i) * p.scale_log2;
+      q[h][i] *= p.scale_log2;
       qsum[h] += q[h][i];
     }
   }
@@ -161,72 +148,87 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
     for (int i = 0; i < E; ++i) o[h][i] = 0.0f;
   }
 
-  for (int base = t_begin + wave * TPS; base < t_end; base += kWaves * TPS) {
-    const int t = base + tok;
-    const bool valid = t < t_end;
-    const int64_t tt = valid ? t : t_end - 1;
+  // Rows are consumed through a ring of kPrefetch register buffers: step u is
+  // computed while the loads of the next kPrefetch-1 steps are in flight
+  // (vmcnt retires them in order).  Step counts are made provably uniform
+  // (readfirstlane) and every load is unconditional with a clamped row index,
+  // so the waitcnt pass sees straight-line code and can wait for just the
+  // oldest buffer instead of draining the queue.
+  constexpr int kStride = kWaves * TPS;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int base0 = t_begin + wv * TPS;
+  const int nsteps = base0 < t_end ? (t_end - base0 + kStride - 1) / kStride : 0;
+  if (nsteps > 0) {
+    const int last = t_end - 1;
+    RowBuf<D, WPL, SB> buf[kPrefetch];
+#pragma unroll
+    for (int u = 0; u < kPrefetch; ++u)
+      buf[u].load(kq, vq, ks, kb, vs, vb, min(base0 + u * kStride + tok, last));
 
-    uint32_t kw[WPL], vw[WPL];
-    load_words<WPL>(kq + tt * RW, kw);
-    load_words<WPL>(vq + tt * RW, vw);
-    const float ksc = sb_to_f32<SB>(ks[tt * NG]);
-    const float kbi = sb_to_f32<SB>(kb[tt * NG]);
-    const float vsc = sb_to_f32<SB>(vs[tt * NG]);
-    const float vbi = sb_to_f32<SB>(vb[tt * NG]);
+    for (int s0 = 0; s0 < nsteps; s0 += kPrefetch) {
+#pragma unroll
+      for (int u = 0; u < kPrefetch; ++u) {
+        const int step = s0 + u;
+        if (step < nsteps) {  // uniform
+          const bool valid = base0 + step * kStride + tok < t_end;
+          const RowBuf<D, WPL, SB>& r = buf[u];
+      const float ksc = sb_to_f32<SB>(r.ks), kbi = sb_to_f32<SB>(r.kb);
+      const float vsc = sb_to_f32<SB>(r.vs), vbi = sb_to_f32<SB>(r.vb);
+      float part[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) part[h] = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WPL; ++w) {
+        float n[8];
+        unpack8(r.kw[w], n);
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) part[h] = fmaf(q[h][w * 8 + i], n[i], part[h]);
+      }
+#pragma unroll
+      for (int h = 0; h < G; ++h) part[h] = ksc * part[h] + kbi * qsum[h];
+#pragma unroll
+      for (int h = 0; h < G; ++h) part[h] = group_sum<LPT>(part[h]);
 
-    float part[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) part[h] = 0.0f;
-#pragma unroll
-    for (int w = 0; w < WPL; ++w) {
-      float n[8];
-      unpack8(kw[w], n);
-#pragma unroll
-      for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) part[h] = fmaf(q[h][w * 8 + i], n[i], part[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) part[h] = ksc * part[h] + kbi * qsum[h];
-#pragma unroll
-    for (int off = 1; off < LPT; off <<= 1)
-#pragma unroll
-      for (int h = 0; h < G; ++h) part[h] += shfl_xor_f(part[h], off);
-
-    bool need = false;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      part[h] = valid ? part[h] : -INFINITY;
-      need |= part[h] > m[h];
-    }
-    if (__any(need)) {
+      bool need = false;
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float mn = fmaxf(m[h], part[h]);
-        const float f = (mn == m[h]) ? 1.0f : fast_exp2(m[h] - mn);
-        l[h] *= f;
-        ob[h] *= f;
-#pragma unroll
-        for (int i = 0; i < E; ++i) o[h][i] *= f;
-        m[h] = mn;
+        part[h] = valid ? part[h] : -INFINITY;
+        need |= part[h] > m[h];
       }
-    }
-    float ps[G];
+      if (__any(need)) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float pp = valid ? fast_exp2(part[h] - m[h]) : 0.0f;
-      l[h] += pp;
-      ob[h] = fmaf(pp, vbi, ob[h]);
-      ps[h] = pp * vsc;
-    }
+        for (int h = 0; h < G; ++h) {
+          const float mn = fmaxf(m[h], part[h]);
+          const float f = (mn == m[h]) ? 1.0f : fast_exp2(m[h] - mn);
+          l[h] *= f;
+          ob[h] *= f;
 #pragma unroll
-    for (int w = 0; w < WPL; ++w) {
-      float n[8];
-      unpack8(vw[w], n);
+          for (int i = 0; i < E; ++i) o[h][i] *= f;
+          m[h] = mn;
+        }
+      }
+      float ps[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h)
+      for (int h = 0; h < G; ++h) {
+        const float pp = valid ? fast_exp2(part[h] - m[h]) : 0.0f;
+        l[h] += pp;
+        ob[h] = fmaf(pp, vbi, ob[h]);
+        ps[h] = pp * vsc;
+      }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[h][w * 8 + i] = fmaf(ps[h], n[i], o[h][w * 8 + i]);
+      for (int w = 0; w < WPL; ++w) {
+        float n[8];
+        unpack8(r.vw[w], n);
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[h][w * 8 + i] = fmaf(ps[h], n[i], o[h][w * 8 + i]);
+      }
+        }
+        buf[u].load(kq, vq, ks, kb, vs, vb, min(base0 + (step + kPrefetch) * kStride + tok, last));
+      }
     }
   }
 
@@ -251,89 +253,27 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
     }
   }
 
-  __shared__ float sm_o[kWaves][G][D];
-  __shared__ float sm_m[kWaves][G];
-  __shared__ float sm_l[kWaves][G];
+  using Fin = Finalize<G, D>;
+  __shared__ float arena[Fin::kArena];
   if (tok == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
 #pragma unroll
-      for (int i = 0; i < E; ++i) sm_o[wave][h][j * E + i] = o[h][i];
+      for (int i = 0; i < E; ++i) Fin::o(arena, wave, h)[j * E + i] = o[h][i];
       if (j == 0) {
-        sm_m[wave][h] = m[h];
-        sm_l[wave][h] = l[h];
+        Fin::m(arena, wave)[h] = m[h];
+        Fin::l(arena, wave)[h] = l[h];
       }
     }
   }
-  __syncthreads();
-
-  const int64_t head_base = static_cast<int64_t>(b) * p.Hq + h0;
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-    const int h = idx / D, d = idx - (idx / D) * D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
-    float O = 0.0f, Ls = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = merge_factor(sm_m[w][h], M);
-      O += sm_o[w][h][d] * f;
-      Ls += sm_l[w][h] * f;
-    }
-    if (S == 1) {
-      p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
-    } else {
-      const int64_t slot = (head_base + h) * p.max_splits + split;
-      p.ws_o[slot * D + d] = O;
-      if (d == 0) {
-        p.ws_ml[slot * 2] = M;
-        p.ws_ml[slot * 2 + 1] = Ls;
-      }
-    }
-  }
-  if (S == 1) return;
-
-  // ---- last workgroup of this (sequence, kv head, subgroup) merges splits ----
-  __threadfence();
-  __syncthreads();
-  __shared__ int s_last;
-  if (threadIdx.x == 0) {
-    int* cnt = p.ws_cnt + static_cast<int64_t>(b) * p.Hq + hy;
-    const int old = atomicAdd(cnt, 1);
-    s_last = (old == S - 1);
-    if (old == S - 1) atomicExch(cnt, 0);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-    const int h = idx / D, d = idx - (idx / D) * D;
-    const int64_t slot0 = (head_base + h) * p.max_splits;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s)
-      M = fmaxf(M, __hip_atomic_load(p.ws_ml + (slot0 + s) * 2, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT));
-    float O = 0.0f, Ls = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const float ms = __hip_atomic_load(p.ws_ml + (slot0 + s) * 2, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-      const float ls = __hip_atomic_load(p.ws_ml + (slot0 + s) * 2 + 1, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-      const float f = merge_factor(ms, M);
-      O += __hip_atomic_load(p.ws_o + (slot0 + s) * D + d, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT) * f;
-      Ls += ls * f;
-    }
-    p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
-  }
+  Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, S, split, b * p.Hq + hy);
 }
 
 // ---- host side ---------------------------------------------------------------
 
 constexpr int kTargetWgs = 1024;
-constexpr int kMinChunk = 64;
-constexpr int kChunkGranule = 32;
+constexpr int kMinChunk = 128;
+constexpr int kChunkGranule = 128;
 
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
@@ -348,11 +288,13 @@ int head_subgroup(int gqa) {
 // Keys per workgroup: enough workgroups to fill 256 CUs several times over,
 // never fewer than kMinChunk rows.
 int plan_chunk(int max_len, int64_t groups) {
+  // never more than kMaxSplits chunks per sequence
+  const int64_t floor_c = (static_cast<int64_t>(max_len) + kMaxSplits - 1) / kMaxSplits;
   const int forced = env_int("TQ_SDPA_CHUNK", 0);
-  if (forced > 0) return forced;
+  if (forced > 0) return static_cast<int>(std::max<int64_t>(forced, floor_c));
   const int64_t want = (static_cast<int64_t>(max_len) * groups + kTargetWgs - 1) / kTargetWgs;
   int64_t c = (want + kChunkGranule - 1) / kChunkGranule * kChunkGranule;
-  c = std::max<int64_t>(c, kMinChunk);
+  c = std::max<int64_t>({c, int64_t{kMinChunk}, floor_c});
   return static_cast<int>(std::min<int64_t>(c, 1 << 30));
 }
 
@@ -361,10 +303,10 @@ int plan_chunk(int max_len, int64_t groups) {
 int max_splits_bound(int max_len, int64_t groups) {
   if (max_len <= 0) return 1;
   const int forced = env_int("TQ_SDPA_CHUNK", 0);
-  if (forced > 0) return (max_len + forced - 1) / forced;
+  if (forced > 0) return std::min((max_len + forced - 1) / forced, kMaxSplits);  // chunk >= ceil(L/kMaxSplits)
   const int64_t by_len = (static_cast<int64_t>(max_len) + kMinChunk - 1) / kMinChunk;
   const int64_t by_wgs = (kTargetWgs + groups - 1) / groups;
-  return static_cast<int>(std::max<int64_t>(1, std::min(by_len, by_wgs)));
+  return static_cast<int>(std::max<int64_t>(1, std::min({by_len, by_wgs, int64_t{kMaxSplits}})));
 }
 
 struct WsLayout {
@@ -461,6 +403,13 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
 
   dim3 grid(max_splits, Hkv * n_sub, batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Matrix-core kernel when it serves (D, G); the VALU kernel otherwise or
+  // when TQ_SDPA_IMPL=valu forces it.
+  const char* impl = std::getenv("TQ_SDPA_IMPL");
+  if (!(impl && std::string(impl) == "valu")) {
+    const int r = launch_sdpa_mfma(p, D, G, sb_dtype, grid, s);
+    if (r >= 0) return r;
+  }
   switch (D) {
     case 128: return launch_d<128>(p, G, sb_dtype, grid, s);
     case 256: return launch_d<256>(p, G, sb_dtype, grid, s);

@@ -1,0 +1,213 @@
+// Shared pieces of the two fused int4 decode-attention kernels (the VALU
+// kernel in tq_sdpa.hip and the matrix-core kernel in tq_sdpa_mfma.hip):
+// launch parameters, the per-sequence key range, q loading, and the
+// workgroup finalisation (cross-wave merge, split-K partials, and the
+// last-workgroup log-sum-exp merge).
+#pragma once
+
+#include <math.h>
+
+#include "tq_internal.h"
+
+namespace tq {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxSplits = 256;  // splits per (sequence, kv head); bounds the merge's LDS
+
+struct SdpaParams {
+  const void* q;
+  int q_dtype;
+  const uint32_t* kq;
+  const void* ks;
+  const void* kb;
+  const uint32_t* vq;
+  const void* vs;
+  const void* vb;
+  float* out;
+  float* ws_o;    // [B][Hq][max_splits][D]
+  float* ws_ml;   // [B][Hq][max_splits][2]
+  int* ws_cnt;    // [B][Hq]  (one counter per (sequence, kv head, head subgroup))
+  int Hq, Hkv, cap, gqa, n_sub;
+  int n;                   // single-sequence length (seq_lens == nullptr)
+  const int* seq_lens;     // device [B] or nullptr
+  const int* windows;      // device [B] or nullptr
+  int window;
+  int n_clamp;             // upper bound applied to every sequence length
+  float scale_log2;        // scale * log2(e)
+  int chunk;
+  int max_splits;
+};
+
+// The keys one workgroup attends: rows [t_begin, t_end) of its sequence's
+// cache.  Key ki survives the reference window rule (skip ki when
+// W > 0 and n-1-ki >= W, lib/turboquant.metal:779) iff ki >= n - W.
+struct SplitRange {
+  int S;        // number of splits of this sequence (>= 1)
+  int t_begin;  // first row of this split
+  int t_end;    // one past the last row
+};
+
+__device__ __forceinline__ SplitRange split_range(const SdpaParams& p, int b, int split) {
+  int n_b = p.seq_lens ? p.seq_lens[b] : p.n;
+  n_b = min(n_b, p.n_clamp);
+  const int W = p.windows ? p.windows[b] : p.window;
+  const int lo = W > 0 ? max(0, n_b - W) : 0;
+  const int L = max(n_b - lo, 0);
+  SplitRange r;
+  r.S = L > 0 ? (L + p.chunk - 1) / p.chunk : 1;
+  r.t_begin = lo + split * p.chunk;
+  r.t_end = min(r.t_begin + p.chunk, n_b);
+  return r;
+}
+
+// E contiguous elements of a q row, any of the three input dtypes (one
+// uniform branch, then straight-line 16 B loads).
+template <int E, bool kF16>
+__device__ __forceinline__ void load_q16(const uint16_t* p, float out[E]) {
+  const uint4* v4 = reinterpret_cast<const uint4*>(p);
+  uint32_t w[E / 2];
+#pragma unroll
+  for (int i = 0; i < E / 8; ++i) {
+    const uint4 v = v4[i];
+    w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+  }
+#pragma unroll
+  for (int k = 0; k < E / 2; ++k) {
+    if constexpr (kF16) {
+      out[2 * k] = __half2float(__ushort_as_half(static_cast<uint16_t>(w[k] & 0xFFFFu)));
+      out[2 * k + 1] = __half2float(__ushort_as_half(static_cast<uint16_t>(w[k] >> 16)));
+    } else {
+      out[2 * k] = __uint_as_float(w[k] << 16);
+      out[2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+    }
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void load_q_slice(const void* q, int dtype, int64_t off, float out[E]) {
+  if (dtype == TQ_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(q) + off);
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i) {
+      const float4 v = p[i];
+      out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+    }
+  } else if (dtype == TQ_F16) {
+    load_q16<E, true>(static_cast<const uint16_t*>(q) + off, out);
+  } else {
+    load_q16<E, false>(static_cast<const uint16_t*>(q) + off, out);
+  }
+}
+
+// Agent-scope (all XCDs) coherent store / load of split-K partials.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float merge_factor(float m, float M) {
+  return m == -INFINITY ? 0.0f : fast_exp2(m - M);
+}
+
+// LDS arena of the finalisation: [o: kWaves*G*D | m: kWaves*G | l: kWaves*G],
+// later reused for the per-split (m, l) of the last workgroup.
+template <int G, int D>
+struct Finalize {
+  static constexpr int kArena = (kWaves * G * D + 2 * kWaves * G) > (2 * G * kMaxSplits)
+                                    ? (kWaves * G * D + 2 * kWaves * G)
+                                    : (2 * G * kMaxSplits);
+  __device__ static float* o(float* arena, int w, int h) { return arena + (w * G + h) * D; }
+  __device__ static float* m(float* arena, int w) { return arena + kWaves * G * D + w * G; }
+  __device__ static float* l(float* arena, int w) {
+    return arena + kWaves * G * D + kWaves * G + w * G;
+  }
+
+  // Called by all threads after every wave stored its unnormalised output
+  // O[h][d] (relative to its running max m[h]) and denominator l[h] into the
+  // arena (no barrier needed before the call).  head_base = b*Hq + first head.
+  __device__ static void run(const SdpaParams& p, float* arena, int64_t head_base, int S,
+                             int split, int counter) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+      const int h = idx / D, d = idx - (idx / D) * D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m(arena, w)[h]);
+      float O = 0.0f, Ls = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float f = merge_factor(m(arena, w)[h], M);
+        O += o(arena, w, h)[d] * f;
+        Ls += l(arena, w)[h] * f;
+      }
+      if (S == 1) {
+        p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+      } else {
+        const int64_t slot = (head_base + h) * p.max_splits + split;
+        store_coherent(p.ws_o + slot * D + d, O);
+        if (d == 0) {
+          store_coherent(p.ws_ml + slot * 2, M);
+          store_coherent(p.ws_ml + slot * 2 + 1, Ls);
+        }
+      }
+    }
+    if (S == 1) return;
+
+    // The last workgroup of this (sequence, kv head, subgroup) to finish merges
+    // the splits.  Partials are written with agent-scope stores (write-through
+    // to the coherence point shared by all XCDs) and read with agent-scope
+    // loads, so no L2 write-back/invalidate fence is needed -- such a fence
+    // costs ~4 us per workgroup here.  vmcnt(0) before the barrier makes every
+    // wave's partial stores complete before thread 0 bumps the counter.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    __shared__ int s_last;
+    if (threadIdx.x == 0) {
+      int* cnt = p.ws_cnt + counter;
+      const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (old == S - 1);
+      if (old == S - 1)  // leave the workspace zeroed for the next call
+        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    // Stage every split's (m, l) in LDS, then each thread reduces its
+    // (head, dim) outputs with independent coherent loads.
+    float* s_m = arena;  // the wave-merge data is dead past the barriers above
+    float* s_l = arena + G * kMaxSplits;
+    for (int i = threadIdx.x; i < G * S; i += kThreads) {
+      const int h = i / S, sp = i - (i / S) * S;
+      const int64_t slot = (head_base + h) * p.max_splits + sp;
+      s_m[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2);
+      s_l[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2 + 1);
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+      const int h = idx / D, d = idx - (idx / D) * D;
+      const float* ms = s_m + h * kMaxSplits;
+      const float* ls = s_l + h * kMaxSplits;
+      float M = -INFINITY;
+      for (int sp = 0; sp < S; ++sp) M = fmaxf(M, ms[sp]);
+      const float* po = p.ws_o + (head_base + h) * p.max_splits * D + d;
+      float O = 0.0f, Ls = 0.0f;
+#pragma unroll 8
+      for (int sp = 0; sp < S; ++sp) {
+        const float f = merge_factor(ms[sp], M);
+        O = fmaf(load_coherent(po + static_cast<int64_t>(sp) * D), f, O);
+        Ls = fmaf(ls[sp], f, Ls);
+      }
+      p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+    }
+  }
+};
+
+// Launch of the matrix-core kernel (tq_sdpa_mfma.hip).  Returns TQ_OK,
+// a tq_status error, or -1 when (D, G) is not served by that kernel.
+int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
+                     hipStream_t stream);
+
+}  // namespace tq

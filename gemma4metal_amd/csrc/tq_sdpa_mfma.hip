@@ -1,0 +1,462 @@
+// Fused int4-KV decode attention on the CDNA4 matrix cores (gfx950).
+//
+// Same contract, work split and finalisation as the VALU kernel in
+// tq_sdpa.hip (replaces sdpa_int4_vector, lib/turboquant.metal:723-889); the
+// difference is where the multiply-accumulates run.  Each wave64 consumes 32
+// keys per iteration:
+//
+// K . q  -- v_mfma_i32_16x16x64_i8.  A = 16 keys x 64 dims of nibbles as int8
+//   (two ANDs and a shift split a word into 8 int8 lanes), B = q as three
+//   signed base-256 digits of round(q * 2^F) (22-bit fixed point per head) in
+//   16 columns (head h, quant group g); each B column is zero outside its
+//   group's dims, so C[key][(h,g)] is the exact integer partial dot of group g.
+//   The fp32 score is sum_g s_g * 2^-F * dot_g + b_g * sum(q over g), the
+//   (h,g) columns being folded with a DPP butterfly.
+// P . V  -- v_mfma_f32_16x16x32_f16.  A = 16 dims x 32 keys, built by
+//   v_perm_b32 gathering one byte of two keys' words and an and-or with the
+//   fp16 magic 0x6400 (1024 + nibble); B = the softmax weights p*s_v*1024
+//   split into fp16 hi + lo parts (22-bit), again in (h,g) columns.  The 1024
+//   offset is removed at the end from the running sum of the weights.
+//
+// Lane roles (l = lane, m = l % 16, c = l / 16; layouts checked on hardware):
+//   A rows / B cols / C cols = m;  k-slot j of lane-group c is k = 8c + j
+//   (f16) or 16c + 4v + byte (i8);  C rows held by lane-group c: 4c .. 4c+3.
+//   Key of V slot j in lane-group c: t0 + 16*(j/4) + 4c + (j%4), which is the
+//   K tile (j/4), C row 4c + (j%4): the softmax weights are produced by the
+//   K MFMAs exactly in the lanes and slots the V MFMAs consume them from.
+//
+// Scale/bias of 32 keys are staged through 1 KB of LDS per wave, transposed
+// to [array][group][key] so each lane reads its 8 values with two 8 B reads.
+// Loads are double-buffered one iteration (9 KB per wave) ahead.
+#include "tq_sdpa_common.h"
+
+namespace tq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+template <int D, int G>
+struct MGeom {
+  static constexpr int NG = D / 64;     // quant groups per row
+  static constexpr int COLS = G * NG;   // used MFMA columns
+  static constexpr int KW = D / 32;     // K words per lane per key (D/8 bytes)
+  static constexpr int KM = D / 64;     // int8 MFMAs per 16-key tile (2 words each)
+  static constexpr int VW = D / 128;    // V words per lane per key
+  static constexpr int VM = 8 * VW;     // f16 MFMAs per iteration (= D/16)
+  static constexpr int SCW = NG / 2;    // 32-bit words of one key's scales
+  static_assert(COLS <= 16, "more than 16 (head, group) columns");
+  static_assert(D == 128 || D == 256, "D");
+};
+
+template <int D>
+struct IterBuf {
+  uint32_t kw[2][D / 32];   // [tile][word] K slice of key (t0 + 16*tile + m)
+  uint32_t vw[8][D / 128];  // [slot][word]  V words of key(slot)
+  uint32_t sc[2][D / 128];  // scales of keys (t0 + 2k, t0 + 2k + 1) of array l/16
+};
+
+// Per-lane row offsets (in keys) inside one 32-key iteration.
+struct LaneRows {
+  int k[2];   // K rows of tiles 0, 1
+  int v[8];   // V rows of slots 0..7
+  int s[2];   // scale rows of this lane's key pair
+};
+
+// Loads of one iteration starting at key t0: every row index is clamped to
+// `last` with one v_min against a uniform limit (only the final, partial
+// iteration of a wave is affected), and addressed as a uniform base plus a
+// 32-bit lane offset.
+template <int D, int G>
+__device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0,
+                                          const uint32_t* vq_row0, const uint32_t* sc_arr,
+                                          const LaneRows& lr, int t0, int last, int m, int c) {
+  using Gm = MGeom<D, G>;
+  constexpr uint32_t RB = D / 2;  // bytes per packed row
+  const int lim = last - t0;      // uniform; >= 0 for every issued iteration
+  const char* kb = reinterpret_cast<const char*>(kq_row0 + static_cast<int64_t>(t0) * (D / 8));
+  const char* vb = reinterpret_cast<const char*>(vq_row0 + static_cast<int64_t>(t0) * (D / 8));
+  const char* sb = reinterpret_cast<const char*>(sc_arr + static_cast<int64_t>(t0) * Gm::SCW);
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const uint32_t off = static_cast<uint32_t>(min(lr.k[tile], lim)) * RB + c * Gm::KW * 4;
+#pragma unroll
+    for (int w = 0; w < Gm::KW; w += 4) {
+      const uint4 u = *reinterpret_cast<const uint4*>(kb + off + w * 4);
+      B.kw[tile][w] = u.x; B.kw[tile][w + 1] = u.y; B.kw[tile][w + 2] = u.z; B.kw[tile][w + 3] = u.w;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t off = static_cast<uint32_t>(min(lr.v[j], lim)) * RB + m * Gm::VW * 4;
+    if constexpr (Gm::VW == 2) {
+      const uint2 u = *reinterpret_cast<const uint2*>(vb + off);
+      B.vw[j][0] = u.x; B.vw[j][1] = u.y;
+    } else {
+      B.vw[j][0] = *reinterpret_cast<const uint32_t*>(vb + off);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint32_t off = static_cast<uint32_t>(min(lr.s[e], lim)) * (Gm::SCW * 4);
+    if constexpr (Gm::SCW == 2) {
+      const uint2 u = *reinterpret_cast<const uint2*>(sb + off);
+      B.sc[e][0] = u.x; B.sc[e][1] = u.y;
+    } else {
+      B.sc[e][0] = *reinterpret_cast<const uint32_t*>(sb + off);
+    }
+  }
+}
+
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  return __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  return __half2float(__ushort_as_half(static_cast<uint16_t>(w >> 16)));
+}
+
+// Wave-wide reductions (64 lanes), result in every lane.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor_f(v, off));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_int4_mfma_kernel(SdpaParams p) {
+  using Gm = MGeom<D, G>;
+  constexpr int NG = Gm::NG, COLS = Gm::COLS, KM = Gm::KM, VW = Gm::VW, VM = Gm::VM;
+  constexpr int RW = D / 8;
+  constexpr int NE = (G * D + kThreads - 1) / kThreads;  // q elements per thread
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, c = lane >> 4;  // A row / B,C column; lane group
+  const int n = m;                         // this lane's (head, group) column
+  const int hn = n / NG, gn = n - (n / NG) * NG;
+  const bool col_used = n < COLS;
+  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+
+  const SplitRange rg = split_range(p, b, split);
+  if (split >= rg.S) return;
+  const int t_begin = rg.t_begin, t_end = rg.t_end;
+
+  using Fin = Finalize<G, D>;
+  __shared__ float arena[Fin::kArena];
+  __shared__ uint32_t sc_lds[kWaves][4][NG][16];  // [wave][array][group][key pair] fp16x2
+  __shared__ uint4 bk_lds[3][KM][64];            // B operands of the K MFMAs
+  __shared__ float red_max[NE][kWaves];
+  __shared__ float sh_qhat[G][NG];
+  __shared__ int sh_F[G];
+
+  // ---- first loads, issued before the prologue to overlap its latency ------
+  const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
+  const uint32_t* kq_row0 = p.kq + row0 * RW;
+  const uint32_t* vq_row0 = p.vq + row0 * RW;
+  // (a select chain over kernel-argument pointers keeps the global address
+  // space visible: a lane-indexed pointer table would turn these into FLAT
+  // loads, which the waitcnt logic cannot order and drains with vmcnt(0))
+  const int arr = lane >> 4, k16 = lane & 15;  // this lane's scale array / key pair
+  const void* sc_base = arr == 0 ? p.ks : (arr == 1 ? p.kb : (arr == 2 ? p.vs : p.vb));
+  const uint32_t* sc_arr = static_cast<const uint32_t*>(sc_base) + row0 * Gm::SCW;
+  LaneRows lr;
+  lr.k[0] = m;
+  lr.k[1] = 16 + m;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) lr.v[j] = 16 * (j >> 2) + 4 * c + (j & 3);
+  lr.s[0] = 2 * k16;
+  lr.s[1] = 2 * k16 + 1;
+
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int base0 = t_begin + wv * 32;
+  const int nit = base0 < t_end ? (t_end - base0 + 127) / 128 : 0;
+  const int last = t_end - 1;
+  IterBuf<D> bufA, bufB;
+  if (nit > 0) load_iter<D, G>(bufA, kq_row0, vq_row0, sc_arr, lr, base0, last, m, c);
+
+  // ---- prologue: q as 22-bit fixed point per head, B operands via LDS ------
+  float qv[NE];
+  {
+    const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      const int e = threadIdx.x + k * kThreads;
+      qv[k] = e < G * D ? load_any(p.q, p.q_dtype, qbase + e) * p.scale_log2 : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const float mx = wave_max(fabsf(qv[k]));
+    if (lane == 0) red_max[k][wave] = mx;
+  }
+  {
+    uint4* z = &bk_lds[0][0][0];
+    for (int i = threadIdx.x; i < 3 * KM * 64; i += kThreads) z[i] = uint4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+  // Every wave slot (k, w) holds 64 consecutive elements: one quant group of
+  // one head, since 64 | D and 64 | kThreads.
+  uint8_t* bk_bytes = reinterpret_cast<uint8_t*>(&bk_lds[0][0][0]);
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e0 = wave * 64 + k * kThreads;  // first element of this wave slot
+    if (e0 < G * D) {                          // wave-uniform
+      const int h = e0 / D;
+      float hm = 0.0f;
+#pragma unroll
+      for (int k2 = 0; k2 < NE; ++k2)
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves; ++w2) {
+          const int f0 = w2 * 64 + k2 * kThreads;
+          if (f0 < G * D && f0 / D == h) hm = fmaxf(hm, red_max[k2][w2]);
+        }
+      int ex = 0;
+      if (hm > 0.0f) frexpf(hm, &ex);  // hm < 2^ex
+      const int F = 22 - ex;           // |round(q * 2^F)| <= 2^22
+      const int X = static_cast<int>(__builtin_rintf(qv[k] * ldexpf(1.0f, F)));
+      const int d = (e0 - h * D) + lane;
+      // scatter the three base-256 digits into the B image of lane (16c + n)
+      const int nn = h * NG + (d >> 6), cc = d / (D / 4), off = d % (D / 4);
+      const int i = off >> 4, r16 = off & 15, nib = r16 & 7;
+      const int v = 2 * (r16 >> 3) + (nib & 1), by = nib >> 1;
+      const int byte0 = ((i * 64 + 16 * cc + nn) * 16) + v * 4 + by;
+      const int d0 = static_cast<int8_t>(X & 0xFF);
+      const int X1 = (X - d0) >> 8;
+      const int d1 = static_cast<int8_t>(X1 & 0xFF);
+      const int d2 = (X1 - d1) >> 8;
+      bk_bytes[byte0] = static_cast<uint8_t>(d0);
+      bk_bytes[byte0 + KM * 64 * 16] = static_cast<uint8_t>(d1);
+      bk_bytes[byte0 + 2 * KM * 64 * 16] = static_cast<uint8_t>(d2);
+      const int gsum = wave_sum_i(X);  // exact: 64 * 2^22 < 2^31
+      if (lane == 0) {
+        sh_qhat[h][d >> 6] = static_cast<float>(gsum) * ldexpf(1.0f, -F);
+        if ((d >> 6) == 0) sh_F[h] = F;
+      }
+    }
+  }
+  __syncthreads();
+  const float sf = col_used ? ldexpf(1.0f, -sh_F[hn]) : 0.0f;
+  const float qhat = col_used ? sh_qhat[hn][gn] : 0.0f;
+
+  // ---- main loop ----------------------------------------------------------
+  float m_run = -INFINITY, l_run = 0.0f, wsum = 0.0f, bacc = 0.0f;
+  v4f cv[VM];
+#pragma unroll
+  for (int f = 0; f < VM; ++f) cv[f] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // fp16 magic of (1024 + nibble), kept in a VGPR so each A-operand word is
+  // one v_and_or_b32 (a gfx9 VOP3 instruction takes at most one literal/SGPR)
+  uint32_t magic = 0x64006400u;
+  asm volatile("" : "+v"(magic));
+
+  auto process = [&](const IterBuf<D>& B, int t0) {
+    // scales -> LDS [array][group][key], then this lane's 8 keys x 4 arrays
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const uint32_t a0 = B.sc[0][g >> 1], a1 = B.sc[1][g >> 1];
+      const uint32_t v = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u))
+                                 : ((a0 & 0xFFFFu) | (a1 << 16));
+      sc_lds[wv][arr][g][k16] = v;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t scv[4][2][2];  // [array][tile][pair] = keys 16*tile + 4c + {0,1} / {2,3}
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        const uint2 u = *reinterpret_cast<const uint2*>(&sc_lds[wv][a][gn][8 * tile + 2 * c]);
+        scv[a][tile][0] = u.x;
+        scv[a][tile][1] = u.y;
+      }
+
+    // K . q on the int8 matrix cores, 16 keys per tile
+    float sc[8];
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+      v4i acc[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) acc[k] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < KM; ++i) {
+        const uint32_t w0 = B.kw[tile][2 * i], w1 = B.kw[tile][2 * i + 1];
+        const v4i a = v4i{static_cast<int>(w0 & 0x0F0F0F0Fu),
+                          static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
+                          static_cast<int>(w1 & 0x0F0F0F0Fu),
+                          static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          // B operands live in LDS (16 B per lane per MFMA) to keep the wave
+          // within 256 registers
+          const uint4 u = bk_lds[k][i][lane];
+          const v4i bq = v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z),
+                             static_cast<int>(u.w)};
+          acc[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, acc[k], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
+        const int lo01 = acc[0][i] + (acc[1][i] << 8);
+        const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc[2][i]);
+        const uint32_t kspair = scv[0][tile][i >> 1], kbpair = scv[1][tile][i >> 1];
+        const float ks = (i & 1) ? half_hi(kspair) : half_lo(kspair);
+        const float kb = (i & 1) ? half_hi(kbpair) : half_lo(kbpair);
+        float part = dot * (ks * sf) + kb * qhat;
+        part = group_sum<NG>(part);
+        const int t = t0 + 16 * tile + 4 * c + i;
+        sc[4 * tile + i] = (t < t_end && col_used) ? part : -INFINITY;
+      }
+    }
+
+    // online softmax over the 32 keys (log2 domain); the weights are kept
+    // scaled by 2^10 (p' = exp2(s - m + 10)) so their fp16 hi/lo split stays
+    // in the normal range -- the same factor is in l, so it cancels.
+    float mt = sc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    if (__any(m_new > m_run)) {
+      const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
+      l_run *= f;
+      wsum *= f;
+      bacc *= f;
+#pragma unroll
+      for (int ff = 0; ff < VM; ++ff) cv[ff] *= f;
+      m_run = m_new;
+    }
+    const float m10 = m_run - 10.0f;
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int tile = j >> 2, i = j & 3;
+      const float pj = sc[j] == -INFINITY ? 0.0f : fast_exp2(sc[j] - m10);
+      l_run += pj;
+      const uint32_t vspair = scv[2][tile][i >> 1], vbpair = scv[3][tile][i >> 1];
+      const float vs = (i & 1) ? half_hi(vspair) : half_lo(vspair);
+      const float vb = (i & 1) ? half_hi(vbpair) : half_lo(vbpair);
+      bacc = fmaf(pj, vb, bacc);
+      const float w = pj * vs;
+      hi[j] = static_cast<_Float16>(w);
+      lo[j] = static_cast<_Float16>(w - static_cast<float>(hi[j]));
+      wsum += w;
+    }
+    const v8h bhi = v8h{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+    const v8h blo = v8h{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+    const v8h sixteenth = v8h{0.0625f16, 0.0625f16, 0.0625f16, 0.0625f16,
+                              0.0625f16, 0.0625f16, 0.0625f16, 0.0625f16};
+    const v8h bhi16 = bhi * sixteenth, blo16 = blo * sixteenth;
+
+    // P . V on the f16 matrix cores: A = (1024 + nibble) of 16 dims x 32 keys
+#pragma unroll
+    for (int s = 0; s < VW; ++s) {
+#pragma unroll
+      for (int by = 0; by < 4; ++by) {
+        const uint32_t sel = static_cast<uint32_t>(by) | (0x0Cu << 8) |
+                             (static_cast<uint32_t>(4 + by) << 16) | (0x0Cu << 24);
+        uint32_t alo[4], ahi[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t x = __builtin_amdgcn_perm(B.vw[2 * r + 1][s], B.vw[2 * r][s], sel);
+          alo[r] = (x & 0x000F000Fu) | magic;
+          ahi[r] = (x & 0x00F000F0u) | magic;
+        }
+        const v4i ilo = v4i{static_cast<int>(alo[0]), static_cast<int>(alo[1]),
+                            static_cast<int>(alo[2]), static_cast<int>(alo[3])};
+        const v4i ihi = v4i{static_cast<int>(ahi[0]), static_cast<int>(ahi[1]),
+                            static_cast<int>(ahi[2]), static_cast<int>(ahi[3])};
+        const v8h a_lo = __builtin_bit_cast(v8h, ilo);
+        const v8h a_hi = __builtin_bit_cast(v8h, ihi);
+        const int fe = 8 * s + 2 * by, fo = fe + 1;
+        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, bhi, cv[fe], 0, 0, 0);
+        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, bhi16, cv[fo], 0, 0, 0);
+        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, blo, cv[fe], 0, 0, 0);
+        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, blo16, cv[fo], 0, 0, 0);
+      }
+    }
+  };
+
+  auto load_next = [&](IterBuf<D>& B, int t0) {
+    load_iter<D, G>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c);
+  };
+
+  if (nit > 0) {
+    for (int it = 0; it < nit; it += 2) {
+      load_next(bufB, base0 + (it + 1) * 128);
+      __builtin_amdgcn_sched_barrier(0);
+      process(bufA, base0 + it * 128);
+      __builtin_amdgcn_sched_barrier(0);
+      load_next(bufA, base0 + (it + 2) * 128);
+      __builtin_amdgcn_sched_barrier(0);
+      if (it + 1 < nit) process(bufB, base0 + (it + 1) * 128);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- per-wave result into the finalisation arena --------------------------
+  // The V MFMAs contract over the keys of all four lane groups, so the
+  // per-lane sums (softmax denominator, weight sum of the 1024 offset, bias
+  // term) are totalled over the lane groups of the same column.
+  float l_sum = l_run + shfl_xor_f(l_run, 16);
+  l_sum += shfl_xor_f(l_sum, 32);
+  wsum += shfl_xor_f(wsum, 16);
+  wsum += shfl_xor_f(wsum, 32);
+  bacc += shfl_xor_f(bacc, 16);
+  bacc += shfl_xor_f(bacc, 32);
+  if (col_used) {
+#pragma unroll
+    for (int s = 0; s < VW; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int dim = 8 * (VW * (4 * c + i) + s) + j;
+          if ((dim >> 6) == gn) {
+            const float off = (j & 1) ? 64.0f : 1024.0f;
+            Fin::o(arena, wave, hn)[dim] = (cv[8 * s + j][i] - off * wsum) + bacc;
+          }
+        }
+    if (gn == 0 && c == 0) {
+      Fin::m(arena, wave)[hn] = m_run;
+      Fin::l(arena, wave)[hn] = l_sum;
+    }
+  }
+  Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
+}
+
+template <int D, int G>
+int launch_dg(const SdpaParams& p, dim3 grid, hipStream_t s) {
+  sdpa_int4_mfma_kernel<D, G><<<grid, kThreads, 0, s>>>(p);
+  TQ_CHECK_LAUNCH("sdpa_int4_mfma_kernel");
+  return TQ_OK;
+}
+
+}  // namespace
+
+int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
+                     hipStream_t stream) {
+  if (sb_dtype != TQ_F16) return -1;
+  if (D == 256) {
+    if (G == 1) return launch_dg<256, 1>(p, grid, stream);
+    if (G == 2) return launch_dg<256, 2>(p, grid, stream);
+    if (G == 4) return launch_dg<256, 4>(p, grid, stream);
+  } else if (D == 128) {
+    if (G == 1) return launch_dg<128, 1>(p, grid, stream);
+    if (G == 2) return launch_dg<128, 2>(p, grid, stream);
+    if (G == 4) return launch_dg<128, 4>(p, grid, stream);
+    if (G == 8) return launch_dg<128, 8>(p, grid, stream);
+  }
+  return -1;
+}
+
+}  // namespace tq
