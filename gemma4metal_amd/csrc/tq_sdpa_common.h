@@ -169,8 +169,10 @@ struct Finalize {
       int* cnt = p.ws_cnt + counter;
       const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = (old == S - 1);
-      if (old == S - 1)  // leave the workspace zeroed for the next call
-        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // leave the workspace zeroed for the next call -- with an atomic RMW,
+      // the same kind of operation as the increments (a plain store, even a
+      // write-through one, is not ordered with them)
+      if (old == S - 1) __hip_atomic_exchange(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;

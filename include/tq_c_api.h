@@ -64,7 +64,10 @@ int tq_sync(void);
  *   kv_capacity >= kv_len is the row stride of each head (== kv_len for a
  *   tight [Hkv, N, .] tensor as in the reference).
  * workspace: >= tq_sdpa_int4_workspace_size(...) bytes, zero-filled once
- * before first use (the kernels leave it zeroed again). */
+ * before first use.  Its first 256 KiB hold split counters that every call
+ * returns to zero, so one workspace may serve calls of any shape one after
+ * another on a stream; calls that run concurrently need separate workspaces.
+ * batch * num_heads must not exceed 65536. */
 size_t tq_sdpa_int4_workspace_size(int batch, int num_heads, int num_kv_heads,
                                    int head_dim, int max_kv_len);
 int tq_sdpa_int4(const void* q, tq_dtype q_dtype,

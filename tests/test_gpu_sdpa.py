@@ -126,3 +126,25 @@ def test_append_then_attend_round_trip(gpu):
     O.kv_append_int4(ref_cache, kn, vn, lens0)
     ref = O.sdpa_int4_ragged(qv, *ref_cache.values(), lens0 + 1, wins, 2)
     assert_close(host(out), ref, "append+attend")
+
+
+def test_workspace_reuse_across_shapes(gpu):
+    """Regression: split counters must be back at zero after every call, so
+    calls with different shapes / split counts sharing one workspace stay
+    correct in any order."""
+    rng = np.random.default_rng(41)
+    cases = []
+    for (B, cap, lens, wins) in [(2, 900, [900, 513], [0, 0]), (3, 1500, [1500, 7, 1025], [1024, 0, 0]),
+                                 (1, 4000, [4000], [0]), (4, 700, [1, 700, 650, 129], [0, 64, 0, 0])]:
+        qd, qv = queries(rng, (B, 32, 256), "bf16")
+        k = O.rms_norm(rng.standard_normal((B, 16, cap, 256)).astype(np.float32))
+        v = rng.standard_normal((B, 16, cap, 256)).astype(np.float32)
+        c = O.quantize_int4(k) + O.quantize_int4(v)
+        ref = O.sdpa_int4_ragged(qv, *c, np.array(lens), np.array(wins), 2)
+        cases.append((qd, [dev(a) for a in c], dev(np.array(lens, np.int32)),
+                      dev(np.array(wins, np.int32)), ref))
+    for rep in range(3):
+        for i in (0, 2, 1, 3, 2, 0):
+            qd, cd, ld, wd, ref = cases[i]
+            out = gpu.sdpa_int4_ragged(qd, *cd, ld, 2, windows=wd)
+            assert_close(host(out), ref, f"rep {rep} case {i}")
