@@ -16,6 +16,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -23,6 +24,22 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_GBS = 8000.0  # MI355X HBM3E, published
+# HBM bytes per launch of the headline kernel, measured with rocprofv3 PMC
+# counters (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, calibrated on plain copy and
+# read kernels of known size); the summary file records the commands.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sdpa_int4_mfma_ctx32k.md")
+
+
+def measured_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                m = re.match(r"traffic_bytes_per_launch = .*= ([\d,]+)", line.strip())
+                if m:
+                    return int(m.group(1).replace(",", ""))
+    except OSError:
+        pass
+    return None
 
 
 def parse():
@@ -32,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8, help="distinct KV sets rotated")
     ap.add_argument("--workload", default="ctx32k",
-                    choices=["ctx32k", "sweep", "sliding50", "ragged"])
+                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream"])
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -140,7 +157,6 @@ def main():
 
             ms_step, ms_launch, ms_med = time_launches(torch, step, args.steps, args.warmup)
             gbs = nbytes / (ms_step * 1e-3) / 1e9
-            gbs_k = nbytes / (ms_launch * 1e-3) / 1e9
             line = {
                 "metric": "int4-KV decode SDPA achieved HBM GB/s at 32k ctx",
                 "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
@@ -154,12 +170,16 @@ def main():
                 "config": {"workload": f"sdpa_int4 decode layer Hq={Hq} Hkv={Hkv} D={D} "
                                        f"L={L} W=0 (BASELINE configs[2])",
                            "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"},
-                "roofline": {"bound": "hbm", "achieved": round(gbs_k, 1), "peak": PEAK_GBS,
-                             "unit": "GB/s", "frac": round(gbs_k / PEAK_GBS, 4),
-                             "traffic": None, "kernel": "sdpa_int4_kernel<256,2,__half>",
+                # the timed region is back-to-back launches of this one kernel
+                # on one stream, so region time / K is its mean launch time
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
+                             "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4),
+                             "traffic": measured_traffic() if L == 32768 else None,
+                             "kernel": "sdpa_int4_mfma_kernel<256,2,8>",
                              "bytes_per_launch": nbytes,
-                             "us_per_launch_mean": round(ms_launch * 1e3, 2),
-                             "us_per_launch_median": round(ms_med * 1e3, 2)},
+                             "us_per_launch": round(ms_step * 1e3, 2),
+                             "us_per_launch_event_bracketed_mean": round(ms_launch * 1e3, 2),
+                             "us_per_launch_event_bracketed_median": round(ms_med * 1e3, 2)},
             }
             if not args.no_cpu and L == lens[0]:
                 s0 = sets[0]
@@ -176,6 +196,40 @@ def main():
             torch.cuda.empty_cache()
         for line in lines:
             emit(line, args)
+        return
+
+    if args.workload == "stream":
+        # Plain streaming kernels of known size: the achievable-bandwidth
+        # reference, and the calibration kernels for the HBM byte counters.
+        nbytes = 1 << 30
+        a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").normal_()
+        bdst = torch.empty_like(a)
+        ms_copy, _, _ = time_launches(torch, lambda i: bdst.copy_(a), args.steps, args.warmup)
+        acc = torch.empty((), dtype=torch.float32, device="cuda")
+        ms_sum, _, _ = time_launches(torch, lambda i: torch.sum(a, dim=0, out=acc), args.steps, args.warmup)
+        copy_gbs = 2 * nbytes / (ms_copy * 1e-3) / 1e9
+        read_gbs = nbytes / (ms_sum * 1e-3) / 1e9
+        # the library's own plain streaming-read kernel, best over grid sizes
+        import ctypes
+        from gemma4metal_amd import _lib
+        sink = torch.empty(65536 * 256, dtype=torch.int32, device="cuda")
+        probe = {}
+        for blocks in (1024, 2048, 4096, 8192):
+            ms_p, _, _ = time_launches(torch, lambda i: _lib.call(
+                "tq_stream_read", ctypes.c_void_p(a.data_ptr()), nbytes,
+                ctypes.c_void_p(sink.data_ptr()), blocks,
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), args.steps, args.warmup)
+            probe[blocks] = round(nbytes / (ms_p * 1e-3) / 1e9, 1)
+        emit({"metric": "achievable HBM streaming bandwidth (torch copy / sum of 1 GiB)",
+              "value": round(read_gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+              "warmup": args.warmup, "ms_per_step": round(ms_sum, 5), "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+              "copy_gbs_read_plus_write": round(copy_gbs, 1),
+              "tq_stream_read_gbs_by_blocks": probe,
+              "read_pct_of_peak": round(100 * read_gbs / PEAK_GBS, 2),
+              "config": {"workload": "torch.sum over 1 GiB f32 (read) and copy_ of 1 GiB "
+                                     "(read+write)", "global_batch": 1, "seq_len": 0,
+                         "parallelism": "none (1 GPU)"}}, args)
         return
 
     if args.workload == "sliding50":

@@ -112,17 +112,19 @@ __device__ __forceinline__ float merge_factor(float m, float M) {
   return m == -INFINITY ? 0.0f : fast_exp2(m - M);
 }
 
-// LDS arena of the finalisation: [o: kWaves*G*D | m: kWaves*G | l: kWaves*G],
-// later reused for the per-split (m, l) of the last workgroup.
-template <int G, int D>
+// LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G], later
+// reused for the per-split (m, l) of the last workgroup.  NW = waves per
+// workgroup.
+template <int G, int D, int NW = kWaves>
 struct Finalize {
-  static constexpr int kArena = (kWaves * G * D + 2 * kWaves * G) > (2 * G * kMaxSplits)
-                                    ? (kWaves * G * D + 2 * kWaves * G)
+  static constexpr int kNT = NW * 64;
+  static constexpr int kArena = (NW * G * D + 2 * NW * G) > (2 * G * kMaxSplits)
+                                    ? (NW * G * D + 2 * NW * G)
                                     : (2 * G * kMaxSplits);
   __device__ static float* o(float* arena, int w, int h) { return arena + (w * G + h) * D; }
-  __device__ static float* m(float* arena, int w) { return arena + kWaves * G * D + w * G; }
+  __device__ static float* m(float* arena, int w) { return arena + NW * G * D + w * G; }
   __device__ static float* l(float* arena, int w) {
-    return arena + kWaves * G * D + kWaves * G + w * G;
+    return arena + NW * G * D + NW * G + w * G;
   }
 
   // Called by all threads after every wave stored its unnormalised output
@@ -131,14 +133,14 @@ struct Finalize {
   __device__ static void run(const SdpaParams& p, float* arena, int64_t head_base, int S,
                              int split, int counter) {
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
       const int h = idx / D, d = idx - (idx / D) * D;
       float M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, m(arena, w)[h]);
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, m(arena, w)[h]);
       float O = 0.0f, Ls = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float f = merge_factor(m(arena, w)[h], M);
         O += o(arena, w, h)[d] * f;
         Ls += l(arena, w)[h] * f;
@@ -181,14 +183,14 @@ struct Finalize {
     // (head, dim) outputs with independent coherent loads.
     float* s_m = arena;  // the wave-merge data is dead past the barriers above
     float* s_l = arena + G * kMaxSplits;
-    for (int i = threadIdx.x; i < G * S; i += kThreads) {
+    for (int i = threadIdx.x; i < G * S; i += kNT) {
       const int h = i / S, sp = i - (i / S) * S;
       const int64_t slot = (head_base + h) * p.max_splits + sp;
       s_m[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2);
       s_l[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2 + 1);
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
       const int h = idx / D, d = idx - (idx / D) * D;
       const float* ms = s_m + h * kMaxSplits;
       const float* ls = s_l + h * kMaxSplits;

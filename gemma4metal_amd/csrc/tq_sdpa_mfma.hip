@@ -33,7 +33,12 @@
 namespace tq {
 namespace {
 
+// Waves per workgroup: 8 = two waves per SIMD at one workgroup per CU.
+constexpr int kMfmaWaves = 8;
+
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
@@ -64,7 +69,9 @@ struct LaneRows {
   int s[2];   // scale rows of this lane's key pair
 };
 
-// Loads of one iteration starting at key t0: every row index is clamped to
+// Loads of one iteration starting at key t0 -- non-temporal (streamed, never
+// re-read; measured ~10% more HBM throughput than default-policy loads on
+// this part): every row index is clamped to
 // `last` with one v_min against a uniform limit (only the final, partial
 // iteration of a wave is affected), and addressed as a uniform base plus a
 // 32-bit lane offset.
@@ -83,7 +90,7 @@ __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0
     const uint32_t off = static_cast<uint32_t>(min(lr.k[tile], lim)) * RB + c * Gm::KW * 4;
 #pragma unroll
     for (int w = 0; w < Gm::KW; w += 4) {
-      const uint4 u = *reinterpret_cast<const uint4*>(kb + off + w * 4);
+      const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off + w * 4));
       B.kw[tile][w] = u.x; B.kw[tile][w + 1] = u.y; B.kw[tile][w + 2] = u.z; B.kw[tile][w + 3] = u.w;
     }
   }
@@ -91,20 +98,20 @@ __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0
   for (int j = 0; j < 8; ++j) {
     const uint32_t off = static_cast<uint32_t>(min(lr.v[j], lim)) * RB + m * Gm::VW * 4;
     if constexpr (Gm::VW == 2) {
-      const uint2 u = *reinterpret_cast<const uint2*>(vb + off);
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vb + off));
       B.vw[j][0] = u.x; B.vw[j][1] = u.y;
     } else {
-      B.vw[j][0] = *reinterpret_cast<const uint32_t*>(vb + off);
+      B.vw[j][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb + off));
     }
   }
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const uint32_t off = static_cast<uint32_t>(min(lr.s[e], lim)) * (Gm::SCW * 4);
     if constexpr (Gm::SCW == 2) {
-      const uint2 u = *reinterpret_cast<const uint2*>(sb + off);
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(sb + off));
       B.sc[e][0] = u.x; B.sc[e][1] = u.y;
     } else {
-      B.sc[e][0] = *reinterpret_cast<const uint32_t*>(sb + off);
+      B.sc[e][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + off));
     }
   }
 }
@@ -128,13 +135,15 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_int4_mfma_kernel(SdpaParams p) {
+  constexpr int kNT = NW * 64;       // threads per workgroup
+  constexpr int kIter = 32 * NW;     // keys per workgroup iteration
   using Gm = MGeom<D, G>;
   constexpr int NG = Gm::NG, COLS = Gm::COLS, KM = Gm::KM, VW = Gm::VW, VM = Gm::VM;
   constexpr int RW = D / 8;
-  constexpr int NE = (G * D + kThreads - 1) / kThreads;  // q elements per thread
+  constexpr int NE = (G * D + kNT - 1) / kNT;  // q elements per thread
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;  // A row / B,C column; lane group
@@ -149,11 +158,11 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   if (split >= rg.S) return;
   const int t_begin = rg.t_begin, t_end = rg.t_end;
 
-  using Fin = Finalize<G, D>;
+  using Fin = Finalize<G, D, NW>;
   __shared__ float arena[Fin::kArena];
-  __shared__ uint32_t sc_lds[kWaves][4][NG][16];  // [wave][array][group][key pair] fp16x2
+  __shared__ uint32_t sc_lds[NW][4][NG][16];  // [wave][array][group][key pair] fp16x2
   __shared__ uint4 bk_lds[3][KM][64];            // B operands of the K MFMAs
-  __shared__ float red_max[NE][kWaves];
+  __shared__ float red_max[NE][NW];
   __shared__ float sh_qhat[G][NG];
   __shared__ int sh_F[G];
 
@@ -177,7 +186,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int base0 = t_begin + wv * 32;
-  const int nit = base0 < t_end ? (t_end - base0 + 127) / 128 : 0;
+  const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
   const int last = t_end - 1;
   IterBuf<D> bufA, bufB;
   if (nit > 0) load_iter<D, G>(bufA, kq_row0, vq_row0, sc_arr, lr, base0, last, m, c);
@@ -188,7 +197,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
-      const int e = threadIdx.x + k * kThreads;
+      const int e = threadIdx.x + k * kNT;
       qv[k] = e < G * D ? load_any(p.q, p.q_dtype, qbase + e) * p.scale_log2 : 0.0f;
     }
   }
@@ -199,23 +208,23 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   }
   {
     uint4* z = &bk_lds[0][0][0];
-    for (int i = threadIdx.x; i < 3 * KM * 64; i += kThreads) z[i] = uint4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < 3 * KM * 64; i += kNT) z[i] = uint4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
   // Every wave slot (k, w) holds 64 consecutive elements: one quant group of
-  // one head, since 64 | D and 64 | kThreads.
+  // one head, since 64 | D and 64 | kNT.
   uint8_t* bk_bytes = reinterpret_cast<uint8_t*>(&bk_lds[0][0][0]);
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
-    const int e0 = wave * 64 + k * kThreads;  // first element of this wave slot
+    const int e0 = wave * 64 + k * kNT;  // first element of this wave slot
     if (e0 < G * D) {                          // wave-uniform
       const int h = e0 / D;
       float hm = 0.0f;
 #pragma unroll
       for (int k2 = 0; k2 < NE; ++k2)
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2) {
-          const int f0 = w2 * 64 + k2 * kThreads;
+        for (int w2 = 0; w2 < NW; ++w2) {
+          const int f0 = w2 * 64 + k2 * kNT;
           if (f0 < G * D && f0 / D == h) hm = fmaxf(hm, red_max[k2][w2]);
         }
       int ex = 0;
@@ -392,13 +401,13 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
   if (nit > 0) {
     for (int it = 0; it < nit; it += 2) {
-      load_next(bufB, base0 + (it + 1) * 128);
+      load_next(bufB, base0 + (it + 1) * kIter);
       __builtin_amdgcn_sched_barrier(0);
-      process(bufA, base0 + it * 128);
+      process(bufA, base0 + it * kIter);
       __builtin_amdgcn_sched_barrier(0);
-      load_next(bufA, base0 + (it + 2) * 128);
+      load_next(bufA, base0 + (it + 2) * kIter);
       __builtin_amdgcn_sched_barrier(0);
-      if (it + 1 < nit) process(bufB, base0 + (it + 1) * 128);
+      if (it + 1 < nit) process(bufB, base0 + (it + 1) * kIter);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -436,7 +445,8 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
 template <int D, int G>
 int launch_dg(const SdpaParams& p, dim3 grid, hipStream_t s) {
-  sdpa_int4_mfma_kernel<D, G><<<grid, kThreads, 0, s>>>(p);
+  constexpr int NW = kMfmaWaves;
+  sdpa_int4_mfma_kernel<D, G, NW><<<grid, NW * 64, 0, s>>>(p);
   TQ_CHECK_LAUNCH("sdpa_int4_mfma_kernel");
   return TQ_OK;
 }

@@ -52,6 +52,12 @@ int tq_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int tq_memset(void* dst, int value, size_t bytes);
 int tq_sync(void);
 
+/* Measurement utility (no counterpart in the reference): a plain streaming
+ * read of `bytes` (multiple of 16) by `blocks` x 256 threads, XOR-folded into
+ * sink[blocks * 256].  The achievable-HBM-bandwidth reference for the
+ * attention kernel's roofline. */
+int tq_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
 /* ---- fused int4 decode attention ------------------------------------------
  * Replaces turboquant::sdpa_int4 (lib/turboquant.h:196-207,
  * lib/turboquant.cpp:367-417).  out[h] = softmax(scale * q[h] . K^T) V over
