@@ -44,6 +44,21 @@ SIGNATURES = {
     "tq_quantize_int4": (I, [P, I, I64, I, I, I, I, P, P, P, I, P]),
     "tq_kv_append_int4": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, P, I, I, P]),
     "tq_dequantize_int4": (I, [P, P, P, I, I64, I, P, P]),
+    "tq_polar_quantize": (I, [P, P, P, P, I64, I, I, P, P, P, P, P, P]),
+    "tq_polar_quantize_packed": (I, [P, P, P, P, I64, I, I, P, P, P, P, P, P]),
+    "tq_polar_dequantize": (I, [P, P, P, P, P, P, P, P, I64, I, I, P, P]),
+    "tq_polar_dequantize_packed": (I, [P, P, P, P, P, P, P, P, I64, I, I, P, P]),
+    "tq_compressed_score": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, F, P, P]),
+    "tq_compressed_score_packed": (I, [P, I, P, P, P, P, P, P, P, I, I, I, I, F, P, P]),
+    "tq_compressed_sdpa_workspace_size": (SZ, [I, I, I, I]),
+    "tq_compressed_sdpa": (I, [P, I, P, P, P, P, P, P, P, P, I, I, I, I, F, P, P, SZ, P]),
+    "tq_polar_rotate": (I, [P, P, I64, I, P, P]),
+    "tq_qjl_query": (I, [P, P, I, P, P]),
+    "tq_polar7_encode": (I, [P, P, P, P, P, I64, P, P, P, P]),
+    "tq_polar7_kv_append": (I, [P, P, P, P, P, P, P, P, I, I, I, P, I, P]),
+    "tq_polar7_score": (I, [P, P, P, P, P, P, I, I, I, I, F, P, P]),
+    "tq_polar7_sdpa_workspace_size": (SZ, [I, I, I]),
+    "tq_polar7_sdpa_int4v": (I, [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, F, I, P, SZ, P]),
 }
 
 

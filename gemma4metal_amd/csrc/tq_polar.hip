@@ -1,0 +1,1411 @@
+// PolarQuant / QJL on gfx950: encoders, decoders, compressed-key scores and
+// compressed-key decode attention (replaces lib/turboquant.metal:8-224,
+// 424-704 and the primitives of lib/turboquant.cpp:11-359).
+//
+// Two key layouts:
+//  * the reference layouts: 16-value blocks, 4 levels, indices unpacked (one
+//    u8 per angle, lib/turboquant.cpp:105-109) or packed (u32 + 3 u8 per
+//    block, lib/turboquant.metal:501-600), one fp16 radius per block, and
+//    caller-supplied codebooks;
+//  * the 7-level layout of BASELINE configs[4] ("polar7"): one 128-value block
+//    per vector -- 64 level-1 angles (4 bits) and 63 angles of levels 2-7
+//    (2 bits) in 12 words, the fp16 radius and the fp16 norm of the QJL
+//    residual in one word, and the 128 sign bits of the QJL residual sketch
+//    in 4 words.
+//
+// The encoders reproduce the float32 oracle bit for bit: atan2, square roots
+// and the rotation / sketch dot products are a fixed sequence of IEEE fp32
+// operations (correctly rounded division and square root, FMA contraction
+// off), so every index decision and sketch bit is reproducible.
+//
+// Scores and attention run one key per lane.  The polar7 score uses two
+// per-head LDS tables built in the workgroup prologue: the q'-premultiplied
+// level-1 table t1[j][k] = q'[2j] cos c_k + q'[2j+1] sin c_k (a level-1 angle
+// costs one gather instead of a cos/sin pair and 2 FMAs per head), and the
+// QJL byte table tq[pos][byte] = sum of (S q')_i over the set bits of the
+// byte (the 128-bit sign dot costs 16 gathers).  Levels 7..2 are decoded
+// top-down with a 4-entry (cos, sin) table.  V is accumulated with lanes
+// owning dimensions; workgroups merge through the shared split-K
+// finalisation of the int4 kernels.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+
+#include "tq_sdpa_common.h"
+
+namespace tq {
+namespace {
+
+// float32 constants of the deterministic atan2 (same values as the oracle)
+constexpr float kPi = 0x1.921fb6p+1f;
+constexpr float kPi2 = 0x1.921fb6p+0f;
+constexpr float kPi4 = 0x1.921fb6p-1f;
+constexpr float kTwoPi = 0x1.921fb6p+2f;
+constexpr float kTanPi8 = 0x1.a8279ap-2f;
+// (-1)^k / (2k+1), k = 1..10
+constexpr float kAtanC[10] = {-0x1.555556p-2f, 0x1.99999ap-3f, -0x1.24924ap-3f, 0x1.c71c72p-4f,
+                              -0x1.745d18p-4f, 0x1.3b13b2p-4f, -0x1.111112p-4f, 0x1.e1e1e2p-5f,
+                              -0x1.af286cp-5f, 0x1.861862p-5f};
+constexpr float kLog2e = 1.4426950408889634f;
+// sqrt(pi/2) / m
+constexpr float kQjlCoef = 0.009791516697777346f;
+constexpr int kP7Words = 12;
+
+// atan2(y, x) in (-pi, pi]: |t| = min/max of |x|, |y|, reduced with
+// atan(t) = pi/4 + atan((t-1)/(t+1)) above tan(pi/8), then the Taylor series
+// of atan to u^21; octant and sign fix-ups as atan2 (signed zeros included).
+__device__ __forceinline__ float atan2_det(float y, float x) {
+#pragma clang fp contract(off)
+  const float ax = fabsf(x), ay = fabsf(y);
+  const float mx = fmaxf(ax, ay), mn = fminf(ax, ay);
+  const float t = mx > 0.0f ? mn / mx : 0.0f;
+  const bool big = t > kTanPi8;
+  const float u = big ? (t - 1.0f) / (t + 1.0f) : t;
+  const float s = u * u;
+  float p = kAtanC[9];
+#pragma unroll
+  for (int k = 8; k >= 0; --k) {
+    p = p * s;
+    p = p + kAtanC[k];
+  }
+  float r = s * p;
+  r = u * r;
+  float a = u + r;
+  if (big) a = kPi4 + a;
+  if (ay > ax) a = kPi2 - a;
+  if (__float_as_uint(x) >> 31) a = kPi - a;
+  if (__float_as_uint(y) >> 31) a = -a;
+  return a;
+}
+
+// nearest codebook entry under |theta - c|, first minimum wins
+// (lib/turboquant.metal:38-42)
+__device__ __forceinline__ int nearest_idx(float th, const float* cb, int n) {
+#pragma clang fp contract(off)
+  float best = 1e10f;
+  int idx = 0;
+  for (int c = 0; c < n; ++c) {
+    const float d = fabsf(th - cb[c]);
+    if (d < best) {
+      best = d;
+      idx = c;
+    }
+  }
+  return idx;
+}
+
+__device__ __forceinline__ float pair_radius(float a, float b) {
+#pragma clang fp contract(off)
+  const float aa = a * a;
+  const float bb = b * b;
+  return sqrtf(aa + bb);
+}
+
+__device__ __forceinline__ float h2f_lo(uint32_t w) {
+  return __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)));
+}
+__device__ __forceinline__ float h2f_hi(uint32_t w) {
+  return __half2float(__ushort_as_half(static_cast<uint16_t>(w >> 16)));
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor_f(v, off));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += shfl_xor_f(v, off);
+  return v;
+}
+
+// ============================================================================
+// Reference layouts: 16-value blocks, 4 levels
+// ============================================================================
+
+struct Enc16Params {
+  const float* x;
+  const float* P;  // D x D preconditioner or null (x already rotated)
+  int64_t n;       // vectors
+  int D;
+  int rows;        // vectors per workgroup
+  const float* cb; // concatenated codebooks of levels 1..4
+  int ncb[4];
+  int cb_off[4];
+  uint8_t *i1, *i2, *i3, *i4;  // unpacked outputs
+  uint32_t* p1;                 // packed outputs
+  uint8_t *p2, *p3, *p4;
+  uint16_t* radii;
+};
+
+// One workgroup per `rows` vectors: the tile is rotated in LDS (y = x P^T,
+// y_i accumulated d = 0..D-1 with separately rounded products and sums),
+// then one thread encodes each 16-value block.
+template <bool kPacked>
+__global__ __launch_bounds__(256) void polar_encode16_kernel(Enc16Params p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) float smem[];
+  const int D = p.D, R = p.rows;
+  float* cbs = smem;       // [4][256]
+  float* xs = smem + 1024; // [R][D]
+  float* ys = xs + R * D;  // [R][D]
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int rows = static_cast<int>(min(static_cast<int64_t>(R), p.n - row0));
+  for (int i = threadIdx.x; i < 1024; i += 256) {
+    const int l = i >> 8, c = i & 255;
+    cbs[i] = c < p.ncb[l] ? p.cb[p.cb_off[l] + c] : 0.0f;
+  }
+  for (int i = threadIdx.x; i < rows * D; i += 256) xs[i] = p.x[row0 * D + i];
+  __syncthreads();
+  const float* y = xs;
+  if (p.P) {
+    for (int o = threadIdx.x; o < rows * D; o += 256) {
+      const int r = o / D, i = o - r * D;
+      const float* pr = p.P + static_cast<int64_t>(i) * D;
+      const float* xr = xs + r * D;
+      float acc = 0.0f;
+      for (int d = 0; d < D; ++d) acc = acc + xr[d] * pr[d];
+      ys[o] = acc;
+    }
+    __syncthreads();
+    y = ys;
+  }
+  const int nb = D / 16;
+  for (int blk = threadIdx.x; blk < rows * nb; blk += 256) {
+    float r[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) r[j] = y[blk * 16 + j];
+    int k1[8], k2[4], k3[2], k4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a = r[2 * j], b = r[2 * j + 1];
+      float th = atan2_det(b, a);
+      if (th < 0.0f) th = th + kTwoPi;
+      k1[j] = nearest_idx(th, cbs, p.ncb[0]);
+      r[j] = pair_radius(a, b);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = r[2 * j], b = r[2 * j + 1];
+      k2[j] = nearest_idx(atan2_det(b, a), cbs + 256, p.ncb[1]);
+      r[j] = pair_radius(a, b);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float a = r[2 * j], b = r[2 * j + 1];
+      k3[j] = nearest_idx(atan2_det(b, a), cbs + 512, p.ncb[2]);
+      r[j] = pair_radius(a, b);
+    }
+    k4 = nearest_idx(atan2_det(r[1], r[0]), cbs + 768, p.ncb[3]);
+    const float rad = pair_radius(r[0], r[1]);
+    const int64_t gb = row0 * nb + blk;
+    if constexpr (kPacked) {
+      uint32_t w1 = 0, w2 = 0, w3 = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w1 |= (static_cast<uint32_t>(k1[j]) & 0xFu) << (4 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w2 |= (static_cast<uint32_t>(k2[j]) & 0x3u) << (2 * j);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) w3 |= (static_cast<uint32_t>(k3[j]) & 0x3u) << (2 * j);
+      p.p1[gb] = w1;
+      p.p2[gb] = static_cast<uint8_t>(w2);
+      p.p3[gb] = static_cast<uint8_t>(w3);
+      p.p4[gb] = static_cast<uint8_t>(k4 & 0x3);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p.i1[gb * 8 + j] = static_cast<uint8_t>(k1[j]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) p.i2[gb * 4 + j] = static_cast<uint8_t>(k2[j]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) p.i3[gb * 2 + j] = static_cast<uint8_t>(k3[j]);
+      p.i4[gb] = static_cast<uint8_t>(k4);
+    }
+    p.radii[gb] = __half_as_ushort(__float2half_rn(rad));
+  }
+}
+
+struct Keys16 {
+  const uint8_t *i1, *i2, *i3, *i4;  // unpacked indices
+  const uint32_t* p1;                 // packed indices
+  const uint8_t *p2, *p3, *p4;
+  const uint16_t* radii;
+};
+
+// indices of one 16-value block
+template <bool kPacked>
+__device__ __forceinline__ void load_block_idx(const Keys16& k, int64_t gb, int k1[8], int k2[4],
+                                               int k3[2], int& k4) {
+  if constexpr (kPacked) {
+    const uint32_t w = k.p1[gb], b2 = k.p2[gb], b3 = k.p3[gb];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) k1[j] = (w >> (4 * j)) & 0xF;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) k2[j] = (b2 >> (2 * j)) & 0x3;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) k3[j] = (b3 >> (2 * j)) & 0x3;
+    k4 = k.p4[gb] & 0x3;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) k1[j] = k.i1[gb * 8 + j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) k2[j] = k.i2[gb * 4 + j];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) k3[j] = k.i3[gb * 2 + j];
+    k4 = k.i4[gb];
+  }
+}
+
+// Top-down decode of one block with the (cos, sin) tables cst[level][256]
+// (lib/turboquant.metal:100-164).
+__device__ __forceinline__ void decode_block16(const float2* cst, float rad, const int k1[8],
+                                               const int k2[4], const int k3[2], int k4,
+                                               float v[16]) {
+  float a[2], b[4], c[8];
+  {
+    const float2 cs = cst[768 + k4];
+    a[0] = rad * cs.x;
+    a[1] = rad * cs.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float2 cs = cst[512 + k3[j]];
+    b[2 * j] = a[j] * cs.x;
+    b[2 * j + 1] = a[j] * cs.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float2 cs = cst[256 + k2[j]];
+    c[2 * j] = b[j] * cs.x;
+    c[2 * j + 1] = b[j] * cs.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float2 cs = cst[k1[j]];
+    v[2 * j] = c[j] * cs.x;
+    v[2 * j + 1] = c[j] * cs.y;
+  }
+}
+
+// (cos, sin) tables of the four levels in LDS: from the caller's tables when
+// given (the reference's "_fast" variants), else cos/sin of the codebook
+// angles (zero beyond each codebook's size, so any u8 index stays in range).
+struct CsSource {
+  const float* cb;   // concatenated codebooks, or null
+  const float* cs;   // concatenated (cos, sin) pairs, or null
+  int ncb[4];
+  int off[4];
+};
+
+template <int NT>
+__device__ __forceinline__ void fill_cs_tables(float2* cst, const CsSource& s) {
+  for (int i = threadIdx.x; i < 1024; i += NT) {
+    const int l = i >> 8, c = i & 255;
+    float2 v = make_float2(0.0f, 0.0f);
+    if (c < s.ncb[l]) {
+      if (s.cs) {
+        v = make_float2(s.cs[2 * (s.off[l] + c)], s.cs[2 * (s.off[l] + c) + 1]);
+      } else {
+        const float th = s.cb[s.off[l] + c];
+        v = make_float2(cosf(th), sinf(th));
+      }
+    }
+    cst[i] = v;
+  }
+}
+
+struct Dec16Params {
+  Keys16 k;
+  CsSource src;
+  const float* P;  // x = y P when non-null
+  float* out;
+  int64_t n;
+  int D;
+  int rows;
+};
+
+template <bool kPacked>
+__global__ __launch_bounds__(256) void polar_decode16_kernel(Dec16Params p) {
+  extern __shared__ __align__(16) float smem[];
+  float2* cst = reinterpret_cast<float2*>(smem);  // [4][256]
+  float* ys = smem + 2048;                        // [R][D]
+  fill_cs_tables<256>(cst, p.src);
+  __syncthreads();
+  const int R = p.rows, D = p.D, nb = D / 16;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int rows = static_cast<int>(min(static_cast<int64_t>(R), p.n - row0));
+  for (int blk = threadIdx.x; blk < rows * nb; blk += 256) {
+    const int64_t gb = row0 * nb + blk;
+    int k1[8], k2[4], k3[2], k4;
+    load_block_idx<kPacked>(p.k, gb, k1, k2, k3, k4);
+    const float rad = __half2float(__ushort_as_half(p.k.radii[gb]));
+    float v[16];
+    decode_block16(cst, rad, k1, k2, k3, k4, v);
+    float* dst = p.P ? ys + blk * 16 : p.out + gb * 16;
+#pragma unroll
+    for (int j = 0; j < 16; j += 4)
+      *reinterpret_cast<float4*>(dst + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  }
+  if (p.P) {
+    __syncthreads();
+    for (int o = threadIdx.x; o < rows * D; o += 256) {
+      const int r = o / D, d = o - r * D;
+      const float* yr = ys + r * D;
+      float acc = 0.0f;
+      for (int i = 0; i < D; ++i) acc = fmaf(yr[i], p.P[static_cast<int64_t>(i) * D + d], acc);
+      p.out[(row0 + r) * D + d] = acc;
+    }
+  }
+}
+
+// ---- reference scores and attention (keys [kv head][n][D/16 blocks]) -------
+
+struct Attn16 {
+  Keys16 k;
+  CsSource src;
+  const float* q;       // [Hq][D] f32
+  const float* values;  // [Hkv][n][D] f32 (attention only)
+  float* scores;        // [Hq][n] (score only)
+  int D;
+  float qscale;         // multiplies q (scale, or scale*log2e for attention)
+};
+
+// scores of key t of kv head kvh for G heads (q pre-scaled in LDS, [G][D])
+template <int D, int G, bool kPacked>
+__device__ __forceinline__ void score16(const Attn16& a, const float2* cst, const float* qs,
+                                        int64_t keyrow, float s[G]) {
+  constexpr int NB = D / 16;
+#pragma unroll
+  for (int g = 0; g < G; ++g) s[g] = 0.0f;
+  for (int blk = 0; blk < NB; ++blk) {
+    const int64_t gb = keyrow * NB + blk;
+    int k1[8], k2[4], k3[2], k4;
+    load_block_idx<kPacked>(a.k, gb, k1, k2, k3, k4);
+    const float rad = __half2float(__ushort_as_half(a.k.radii[gb]));
+    float v[16];
+    decode_block16(cst, rad, k1, k2, k3, k4, v);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float4* q4 = reinterpret_cast<const float4*>(qs + g * D + blk * 16);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 qv = q4[j];
+        s[g] = fmaf(qv.x, v[4 * j], s[g]);
+        s[g] = fmaf(qv.y, v[4 * j + 1], s[g]);
+        s[g] = fmaf(qv.z, v[4 * j + 2], s[g]);
+        s[g] = fmaf(qv.w, v[4 * j + 3], s[g]);
+      }
+    }
+  }
+}
+
+// tq_score_shared (lib/turboquant.metal:424-499) + GQA: one key per thread,
+// 1024 keys per workgroup, grid (key blocks, kv heads * head subgroups).
+template <int D, int G, bool kPacked>
+__global__ __launch_bounds__(256) void polar16_score_kernel(Attn16 a, int n, int gqa, int n_sub) {
+  __shared__ float2 cst[1024];
+  __shared__ __align__(16) float qs[G * D];
+  const int hy = blockIdx.y, kvh = hy / n_sub, sub = hy - (hy / n_sub) * n_sub;
+  const int h0 = kvh * gqa + sub * G;
+  fill_cs_tables<256>(cst, a.src);
+  for (int i = threadIdx.x; i < G * D; i += 256) qs[i] = a.qscale * a.q[static_cast<int64_t>(h0) * D + i];
+  __syncthreads();
+  for (int t = blockIdx.x * 1024 + threadIdx.x; t < min(n, (blockIdx.x + 1) * 1024); t += 256) {
+    float s[G];
+    score16<D, G, kPacked>(a, cst, qs, static_cast<int64_t>(kvh) * n + t, s);
+#pragma unroll
+    for (int g = 0; g < G; ++g) a.scores[static_cast<int64_t>(h0 + g) * n + t] = s[g];
+  }
+}
+
+// sdpa_tq_sequential (lib/turboquant.metal:166-224) as split-K flash decoding
+// + GQA: 64-key tiles per wave (one key per lane), fp32 V with lanes owning
+// dimensions, output acc / (l + 1e-8).
+template <int D, int G, bool kPacked>
+__global__ __launch_bounds__(256) void polar16_sdpa_kernel(SdpaParams p, Attn16 a) {
+  constexpr int NW = 4, VE = D / 64;
+  __shared__ float2 cst[1024];
+  __shared__ __align__(16) float qs[G * D];
+  using Fin = Finalize<G, D, NW>;
+  __shared__ float arena[Fin::kArena];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+  const SplitRange rg = split_range(p, 0, split);
+  if (split >= rg.S) return;
+  fill_cs_tables<256>(cst, a.src);
+  for (int i = threadIdx.x; i < G * D; i += 256) qs[i] = a.qscale * a.q[static_cast<int64_t>(h0) * D + i];
+  __syncthreads();
+
+  float m_run[G], l_run[G], acc[G][VE];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) acc[g][e] = 0.0f;
+  }
+  const int64_t rowbase = static_cast<int64_t>(kvh) * p.cap;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  for (int tb = rg.t_begin + wv * 64; tb < rg.t_end; tb += NW * 64) {
+    const bool valid = tb + lane < rg.t_end;
+    const int t = min(tb + lane, rg.t_end - 1);
+    float s[G], pw[G];
+    score16<D, G, kPacked>(a, cst, qs, rowbase + t, s);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sv = valid ? s[g] : -INFINITY;
+      const float m_new = fmaxf(m_run[g], wave_max_f(sv));
+      if (m_new > m_run[g]) {  // wave-uniform
+        const float f = merge_factor(m_run[g], m_new);
+        l_run[g] *= f;
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[g][e] *= f;
+        m_run[g] = m_new;
+      }
+      pw[g] = valid ? fast_exp2(sv - m_run[g]) : 0.0f;
+      l_run[g] += pw[g];
+    }
+    const int nk = min(64, rg.t_end - tb);
+    for (int kk = 0; kk < nk; ++kk) {
+      const float* vr = a.values + (rowbase + tb + kk) * D + lane;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pw[g]), kk));
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[g][e] = fmaf(pg, vr[64 * e], acc[g][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) Fin::o(arena, wave, g)[lane + 64 * e] = acc[g][e];
+    const float ls = wave_sum_f(l_run[g]);
+    if (lane == 0) {
+      Fin::m(arena, wave)[g] = m_run[g];
+      Fin::l(arena, wave)[g] = ls;
+    }
+  }
+  Fin::run(p, arena, h0, rg.S, split, hy);
+}
+
+// ============================================================================
+// configs[4] layout: 7 levels over one 128-value block + QJL
+// ============================================================================
+
+struct P7EncParams {
+  const float* x;    // [rows][128]
+  const float* P;    // [128][128] or null
+  const float* S;    // [128][128] QJL sketch matrix
+  const float* cb;   // cb1[16] then cb2[4]
+  const float* cs;   // cs1[16][2] then cs2[4][2]
+  int64_t n;
+  // append mapping (positions != null): x is [B][Hkv][n_new][128], outputs are
+  // [B][Hkv][cap][.] and row t of (b, h) goes to positions[b] + t
+  const int32_t* positions;
+  int n_new, cap, Hkv;
+  uint32_t* angles;  // [.][12]
+  uint32_t* norms;   // [.]   fp16 radius | fp16 ||r|| << 16
+  uint32_t* qjl;     // [.][4]
+};
+
+// One wave per vector: lane l holds y[2l], y[2l+1]; level k pairs come from
+// lanes 2j, 2j+1 of level k-1.  Grid-stride over vectors.
+__global__ __launch_bounds__(256) void polar7_encode_kernel(P7EncParams p) {
+#pragma clang fp contract(off)
+  __shared__ float cb[20];
+  __shared__ float2 cs[20];
+  __shared__ float xs[4][128];
+  __shared__ float rs[4][128];
+  if (threadIdx.x < 20) {
+    cb[threadIdx.x] = p.cb[threadIdx.x];
+    cs[threadIdx.x] = make_float2(p.cs[2 * threadIdx.x], p.cs[2 * threadIdx.x + 1]);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave; row < p.n;
+       row += static_cast<int64_t>(gridDim.x) * 4) {
+    int64_t orow = row;
+    if (p.positions) {
+      const int64_t bh = row / p.n_new;
+      const int t = static_cast<int>(row - bh * p.n_new);
+      const int64_t pos = static_cast<int64_t>(p.positions[bh / p.Hkv]) + t;
+      if (pos < 0 || pos >= p.cap) continue;  // wave-uniform
+      orow = bh * p.cap + pos;
+    }
+    const float2 xv = reinterpret_cast<const float2*>(p.x + row * 128)[lane];
+    float y0 = xv.x, y1 = xv.y;
+    if (p.P) {
+      xs[wave][2 * lane] = xv.x;
+      xs[wave][2 * lane + 1] = xv.y;
+      wave_lds_sync();
+      const float* pa = p.P + (2 * lane) * 128;
+      const float* pb = pa + 128;
+      float acc0 = 0.0f, acc1 = 0.0f;
+      for (int d = 0; d < 128; d += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(pa + d);
+        const float4 b4 = *reinterpret_cast<const float4*>(pb + d);
+        const float x0 = xs[wave][d], x1 = xs[wave][d + 1], x2 = xs[wave][d + 2], x3 = xs[wave][d + 3];
+        acc0 = acc0 + x0 * a4.x; acc0 = acc0 + x1 * a4.y; acc0 = acc0 + x2 * a4.z; acc0 = acc0 + x3 * a4.w;
+        acc1 = acc1 + x0 * b4.x; acc1 = acc1 + x1 * b4.y; acc1 = acc1 + x2 * b4.z; acc1 = acc1 + x3 * b4.w;
+      }
+      y0 = acc0;
+      y1 = acc1;
+    }
+    // ---- encode: level 1 (4-bit, wrapped to [0, 2pi)), levels 2..7 (2-bit)
+    int idx[7];
+    float r;
+    {
+      float th = atan2_det(y1, y0);
+      if (th < 0.0f) th = th + kTwoPi;
+      idx[0] = nearest_idx(th, cb, 16);
+      r = pair_radius(y0, y1);
+    }
+#pragma unroll
+    for (int lv = 1; lv < 7; ++lv) {
+      const float a = __shfl(r, (2 * lane) & 63, 64);
+      const float b = __shfl(r, (2 * lane + 1) & 63, 64);
+      idx[lv] = nearest_idx(atan2_det(b, a), cb + 16, 4);
+      r = pair_radius(a, b);
+    }
+    const float R = __shfl(r, 0, 64);
+    const __half R16 = __float2half_rn(R);
+    // ---- decode top-down (the stored bits): child = parent * cos|sin
+    float v = __half2float(R16);
+#pragma unroll
+    for (int lv = 6; lv >= 1; --lv) {
+      const float pv = __shfl(v, lane >> 1, 64);
+      const int pi = __shfl(idx[lv], lane >> 1, 64);
+      const float2 c = cs[16 + pi];
+      v = (lane & 1) ? pv * c.y : pv * c.x;
+    }
+    const float2 c1 = cs[idx[0]];
+    const float yh0 = v * c1.x, yh1 = v * c1.y;
+    const float r0 = y0 - yh0, r1 = y1 - yh1;
+    float nrm = r0 * r0;
+    const float q1 = r1 * r1;
+    nrm = nrm + q1;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) nrm = nrm + shfl_xor_f(nrm, off);
+    const __half rn16 = __float2half_rn(sqrtf(nrm));
+    // ---- QJL sketch: rows lane and lane + 64 of S r
+    rs[wave][2 * lane] = r0;
+    rs[wave][2 * lane + 1] = r1;
+    wave_lds_sync();
+    const float* sa = p.S + lane * 128;
+    const float* sb = sa + 64 * 128;
+    float ka = 0.0f, kb = 0.0f;
+    for (int d = 0; d < 128; d += 4) {
+      const float4 a4 = *reinterpret_cast<const float4*>(sa + d);
+      const float4 b4 = *reinterpret_cast<const float4*>(sb + d);
+      const float e0 = rs[wave][d], e1 = rs[wave][d + 1], e2 = rs[wave][d + 2], e3 = rs[wave][d + 3];
+      ka = ka + e0 * a4.x; ka = ka + e1 * a4.y; ka = ka + e2 * a4.z; ka = ka + e3 * a4.w;
+      kb = kb + e0 * b4.x; kb = kb + e1 * b4.y; kb = kb + e2 * b4.z; kb = kb + e3 * b4.w;
+    }
+    const uint64_t ba = __ballot(ka >= 0.0f);
+    const uint64_t bb = __ballot(kb >= 0.0f);
+    // ---- pack: lanes 0-7 level-1 words, 8-9 level-2, 10 level 3, 11 levels 4-7
+    uint32_t wa = 0, wb = 0, wc = 0, wd = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      wa |= (static_cast<uint32_t>(__shfl(idx[0], (8 * lane + i) & 63, 64)) & 0xFu) << (4 * i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      wb |= (static_cast<uint32_t>(__shfl(idx[1], (16 * (lane - 8) + i) & 63, 64)) & 0x3u) << (2 * i);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      wc |= (static_cast<uint32_t>(__builtin_amdgcn_readlane(idx[2], i)) & 0x3u) << (2 * i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      wd |= (static_cast<uint32_t>(__builtin_amdgcn_readlane(idx[3], i)) & 0x3u) << (2 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      wd |= (static_cast<uint32_t>(__builtin_amdgcn_readlane(idx[4], i)) & 0x3u) << (16 + 2 * i);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      wd |= (static_cast<uint32_t>(__builtin_amdgcn_readlane(idx[5], i)) & 0x3u) << (24 + 2 * i);
+    wd |= (static_cast<uint32_t>(__builtin_amdgcn_readlane(idx[6], 0)) & 0x3u) << 28;
+    const uint32_t w = lane < 8 ? wa : (lane < 10 ? wb : (lane == 10 ? wc : wd));
+    if (lane < kP7Words) p.angles[orow * kP7Words + lane] = w;
+    if (lane < 4) {
+      const uint64_t bits = lane < 2 ? ba : bb;
+      p.qjl[orow * 4 + lane] = static_cast<uint32_t>(bits >> (32 * (lane & 1)));
+    }
+    if (lane == 0)
+      p.norms[orow] = static_cast<uint32_t>(__half_as_ushort(R16)) |
+                      (static_cast<uint32_t>(__half_as_ushort(rn16)) << 16);
+  }
+}
+
+// y = x P^T for rows of 128 (the query rotation q' = P q); fp32, any order.
+__global__ __launch_bounds__(128) void rotate128_kernel(const float* x, const float* P, float* y,
+                                                        int rows) {
+  __shared__ float xs[128];
+  const int r = blockIdx.x, i = threadIdx.x;
+  xs[i] = x[static_cast<int64_t>(r) * 128 + i];
+  __syncthreads();
+  const float* pr = P + i * 128;
+  float acc = 0.0f;
+  for (int d = 0; d < 128; d += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(pr + d);
+    acc = fmaf(xs[d], a.x, acc);
+    acc = fmaf(xs[d + 1], a.y, acc);
+    acc = fmaf(xs[d + 2], a.z, acc);
+    acc = fmaf(xs[d + 3], a.w, acc);
+  }
+  y[static_cast<int64_t>(r) * 128 + i] = acc;
+}
+
+// ---- polar7 scores ------------------------------------------------------------
+
+struct P7Keys {
+  const float* qp;        // [Hq][128] rotated query q' = P q
+  const float* qs;        // [Hq][128] S q'
+  const float* cs;        // cs1[16][2] then cs2[4][2]
+  const uint32_t* angles; // [Hkv][cap][12]
+  const uint32_t* norms;  // [Hkv][cap]
+  const uint32_t* qjl;    // [Hkv][cap][4]
+  float* scores;          // [Hq][n] (score only)
+};
+
+template <int G>
+struct P7Tables {
+  float t1[G][64][16];
+  float tq[G][16][256];
+  float2 cs2[4];
+  float U[G];
+};
+
+// Builds the per-head tables of heads h0 .. h0+G-1 (all threads; the caller
+// synchronises).  Every entry is multiplied by sc.
+template <int G, int NT>
+__device__ __forceinline__ void build_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0, float sc) {
+  for (int i = threadIdx.x; i < G * 1024; i += NT) {
+    const int g = i >> 10, j = (i >> 4) & 63, c = i & 15;
+    const float* q = k.qp + static_cast<int64_t>(h0 + g) * 128;
+    T.t1[g][j][c] = sc * (q[2 * j] * k.cs[2 * c] + q[2 * j + 1] * k.cs[2 * c + 1]);
+  }
+  for (int i = threadIdx.x; i < G * 4096; i += NT) {
+    const int g = i >> 12, pos = (i >> 8) & 15, bits = i & 255;
+    const float* u = k.qs + static_cast<int64_t>(h0 + g) * 128 + 8 * pos;
+    float s = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+      if ((bits >> b) & 1) s += u[b];
+    T.tq[g][pos][bits] = sc * s;
+  }
+  if (threadIdx.x < 4)
+    T.cs2[threadIdx.x] = make_float2(k.cs[32 + 2 * threadIdx.x], k.cs[33 + 2 * threadIdx.x]);
+  if (threadIdx.x >= 64 && threadIdx.x < 64 + G) {
+    const int g = threadIdx.x - 64;
+    const float* u = k.qs + static_cast<int64_t>(h0 + g) * 128;
+    float s = 0.0f;
+    for (int i = 0; i < 128; ++i) s += u[i];
+    T.U[g] = sc * s;
+  }
+}
+
+// Score of one key (its 12 angle words, norms word and sketch words) for the
+// G heads of the tables: sum_j r1_j t1[j][n_j] + coef ||r|| (2 sum tq - U).
+template <int G>
+__device__ __forceinline__ void p7_score(const P7Tables<G>& T, const uint32_t w[12], uint32_t nrm,
+                                         const uint32_t qj[4], float out[G]) {
+  const float R = h2f_lo(nrm), rn = h2f_hi(nrm);
+  float r6[2], r5[4], r4[8], r3[16];
+  {
+    const float2 c = T.cs2[(w[11] >> 28) & 3];
+    r6[0] = R * c.x;
+    r6[1] = R * c.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const float2 c = T.cs2[(w[11] >> (24 + 2 * j)) & 3];
+    r5[2 * j] = r6[j] * c.x;
+    r5[2 * j + 1] = r6[j] * c.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float2 c = T.cs2[(w[11] >> (16 + 2 * j)) & 3];
+    r4[2 * j] = r5[j] * c.x;
+    r4[2 * j + 1] = r5[j] * c.y;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float2 c = T.cs2[(w[11] >> (2 * j)) & 3];
+    r3[2 * j] = r4[j] * c.x;
+    r3[2 * j + 1] = r4[j] * c.y;
+  }
+  float acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = 0.0f;
+#pragma unroll
+  for (int j3 = 0; j3 < 16; ++j3) {
+    const float2 c3 = T.cs2[(w[10] >> (2 * j3)) & 3];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int j2 = 2 * j3 + e;
+      const float r2 = e ? r3[j3] * c3.y : r3[j3] * c3.x;
+      const float2 c2 = T.cs2[(w[8 + j2 / 16] >> (2 * (j2 % 16))) & 3];
+      const float r1a = r2 * c2.x, r1b = r2 * c2.y;
+      const int ja = 2 * j2, jb = 2 * j2 + 1;
+      const uint32_t na = (w[ja / 8] >> (4 * (ja % 8))) & 15;
+      const uint32_t nb = (w[jb / 8] >> (4 * (jb % 8))) & 15;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        acc[g] = fmaf(r1a, T.t1[g][ja][na], acc[g]);
+        acc[g] = fmaf(r1b, T.t1[g][jb][nb], acc[g]);
+      }
+    }
+  }
+  float qa[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qa[g] = 0.0f;
+#pragma unroll
+  for (int pos = 0; pos < 16; ++pos) {
+    const uint32_t byte = (qj[pos / 4] >> (8 * (pos % 4))) & 255;
+#pragma unroll
+    for (int g = 0; g < G; ++g) qa[g] += T.tq[g][pos][byte];
+  }
+  const float cr = kQjlCoef * rn;
+#pragma unroll
+  for (int g = 0; g < G; ++g) out[g] = fmaf(cr, 2.0f * qa[g] - T.U[g], acc[g]);
+}
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void load_p7_key(const P7Keys& k, int64_t row, uint32_t w[12],
+                                            uint32_t& nrm, uint32_t qj[4]) {
+  const u32x4v* a = reinterpret_cast<const u32x4v*>(k.angles + row * kP7Words);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const u32x4v u = __builtin_nontemporal_load(a + i);
+    w[4 * i] = u.x; w[4 * i + 1] = u.y; w[4 * i + 2] = u.z; w[4 * i + 3] = u.w;
+  }
+  nrm = __builtin_nontemporal_load(k.norms + row);
+  const u32x4v u = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(k.qjl + row * 4));
+  qj[0] = u.x; qj[1] = u.y; qj[2] = u.z; qj[3] = u.w;
+}
+
+// Scores only (the compressed_score of configs[4]): one key per thread, 1024
+// keys per workgroup; grid (key blocks, kv heads * head subgroups).
+template <int G>
+__global__ __launch_bounds__(256) void polar7_score_kernel(P7Keys k, int n, int cap, int gqa,
+                                                           int n_sub, float scale) {
+  __shared__ P7Tables<G> T;
+  const int hy = blockIdx.y, kvh = hy / n_sub, sub = hy - (hy / n_sub) * n_sub;
+  const int h0 = kvh * gqa + sub * G;
+  build_p7_tables<G, 256>(T, k, h0, scale);
+  __syncthreads();
+  for (int t = blockIdx.x * 1024 + threadIdx.x; t < min(n, (blockIdx.x + 1) * 1024); t += 256) {
+    uint32_t w[12], nrm, qj[4];
+    load_p7_key(k, static_cast<int64_t>(kvh) * cap + t, w, nrm, qj);
+    float s[G];
+    p7_score<G>(T, w, nrm, qj, s);
+#pragma unroll
+    for (int g = 0; g < G; ++g) k.scores[static_cast<int64_t>(h0 + g) * n + t] = s[g];
+  }
+}
+
+// configs[4] attention: polar7 + QJL scores, softmax, int4 V (group 64,
+// scale/bias SB), split-K.  Per 64-key tile of a wave: one key per lane for
+// the scores; then 16 steps of 4 keys x 16 words for V (lane: key 4*step +
+// lane/16, dims 8*(lane%16) .. +7), weights read back from LDS.
+template <int G, typename SB>
+__global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
+  constexpr int NW = 4, D = 128;
+  __shared__ P7Tables<G> T;
+  using Fin = Finalize<G, D, NW>;
+  __shared__ float arena[Fin::kArena];
+  __shared__ float p_lds[NW][G][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+  const SplitRange rg = split_range(p, 0, split);
+  if (split >= rg.S) return;
+  build_p7_tables<G, NW * 64>(T, k, h0, p.scale_log2);
+  __syncthreads();
+
+  const SB* vs = static_cast<const SB*>(p.vs);
+  const SB* vb = static_cast<const SB*>(p.vb);
+  const int wd = lane & 15, kg = lane >> 4, gq = wd >> 3;
+  float m_run[G], l_run[G], acc[G][8], accb[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.0f;
+    accb[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+  }
+  const int64_t rowbase = static_cast<int64_t>(kvh) * p.cap;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  for (int tb = rg.t_begin + wv * 64; tb < rg.t_end; tb += NW * 64) {
+    const bool valid = tb + lane < rg.t_end;
+    const int t = min(tb + lane, rg.t_end - 1);
+    uint32_t w[12], nrm, qj[4];
+    load_p7_key(k, rowbase + t, w, nrm, qj);
+    float s[G];
+    p7_score<G>(T, w, nrm, qj, s);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sv = valid ? s[g] : -INFINITY;
+      const float m_new = fmaxf(m_run[g], wave_max_f(sv));
+      if (m_new > m_run[g]) {  // wave-uniform
+        const float f = merge_factor(m_run[g], m_new);
+        l_run[g] *= f;
+        accb[g] *= f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] *= f;
+        m_run[g] = m_new;
+      }
+      const float pw = valid ? fast_exp2(sv - m_run[g]) : 0.0f;
+      l_run[g] += pw;
+      p_lds[wave][g][lane] = pw;
+    }
+    wave_lds_sync();
+#pragma unroll 4
+    for (int st = 0; st < 16; ++st) {
+      const int kk = 4 * st + kg;
+      const int64_t vrow = rowbase + min(tb + kk, rg.t_end - 1);
+      const uint32_t wv4 = __builtin_nontemporal_load(p.vq + vrow * 16 + wd);
+      const float sc = sb_to_f32(vs[vrow * 2 + gq]);
+      const float bi = sb_to_f32(vb[vrow * 2 + gq]);
+      const uint32_t lo = wv4 & 0x0F0F0F0Fu, hi = (wv4 >> 4) & 0x0F0F0F0Fu;
+      float nv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nv[2 * i] = static_cast<float>((lo >> (8 * i)) & 0xFFu);
+        nv[2 * i + 1] = static_cast<float>((hi >> (8 * i)) & 0xFFu);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pg = p_lds[wave][g][kk];
+        const float ps = pg * sc;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(ps, nv[j], acc[g][j]);
+        accb[g] = fmaf(pg, bi, accb[g]);
+      }
+    }
+    wave_lds_sync();
+  }
+  // sum the four key groups of each dimension slice, then one lane per slice
+  // writes its 8 dims (the bias term belongs to the slice's quant group)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[g][j] += shfl_xor_f(acc[g][j], 16);
+      acc[g][j] += shfl_xor_f(acc[g][j], 32);
+    }
+    accb[g] += shfl_xor_f(accb[g], 16);
+    accb[g] += shfl_xor_f(accb[g], 32);
+    const float ls = wave_sum_f(l_run[g]);
+    if (lane < 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Fin::o(arena, wave, g)[8 * lane + j] = acc[g][j] + accb[g];
+    }
+    if (lane == 0) {
+      Fin::m(arena, wave)[g] = m_run[g];
+      Fin::l(arena, wave)[g] = ls;
+    }
+  }
+  Fin::run(p, arena, h0, rg.S, split, hy);
+}
+
+// ---- host helpers -----------------------------------------------------------------
+
+// query heads per workgroup of the polar kernels (LDS tables scale with it)
+int polar_subgroup(int gqa, int max_g) {
+  for (int g : {4, 2}) if (g <= max_g && gqa % g == 0) return g;
+  return 1;
+}
+
+// keys per workgroup: about four workgroups per CU, multiples of 256 keys
+int polar_chunk(int L, int64_t groups) {
+  const int64_t floor_c = (static_cast<int64_t>(L) + kMaxSplits - 1) / kMaxSplits;
+  const int64_t want = (static_cast<int64_t>(L) * groups + 4 * target_wgs() - 1) / (4 * target_wgs());
+  int64_t c = (want + 255) / 256 * 256;
+  c = std::max<int64_t>({c, int64_t{256}, floor_c});
+  return static_cast<int>(std::min<int64_t>(c, 1 << 30));
+}
+
+int polar_splits_bound(int L, int64_t groups) {
+  if (L <= 0) return 1;
+  const int64_t by_len = (static_cast<int64_t>(L) + 255) / 256;
+  const int64_t by_wgs = (4 * target_wgs() + groups - 1) / groups;
+  return static_cast<int>(std::max<int64_t>(1, std::min({by_len, by_wgs, int64_t{kMaxSplits}})));
+}
+
+int check_codebooks(const float* cb, const int* ncb, int max_first, int max_rest, CsSource& s,
+                     const char* fn) {
+  TQ_CHECK_ARG(ncb != nullptr, "%s: n_codebook is NULL", fn);
+  int off = 0;
+  for (int l = 0; l < 4; ++l) {
+    const int mx = l == 0 ? max_first : max_rest;
+    TQ_CHECK_ARG(ncb[l] >= 1 && ncb[l] <= mx, "%s: codebook %d size %d not in [1, %d]", fn, l + 1,
+                 ncb[l], mx);
+    s.ncb[l] = ncb[l];
+    s.off[l] = off;
+    off += ncb[l];
+  }
+  s.cb = cb;
+  return TQ_OK;
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+// ============================================================================
+// C ABI
+// ============================================================================
+
+namespace {
+
+int encode16_common(const float* x, const float* P, const float* codebooks, const int* n_codebook,
+                    int64_t n, int D, int block_size, bool packed, uint8_t* i1, uint8_t* i2,
+                    uint8_t* i3, uint8_t* i4, uint32_t* p1, uint8_t* p2, uint8_t* p3, uint8_t* p4,
+                    uint16_t* radii, void* stream, const char* fn) {
+  if (block_size != 16) {
+    set_error("%s: block_size must be 16 (the reference kernels hard-code it)", fn);
+    return TQ_ERR_UNSUPPORTED;
+  }
+  TQ_CHECK_ARG(D >= 16 && D <= 2048 && D % 16 == 0, "%s: dim must be a multiple of 16 in [16, 2048]", fn);
+  TQ_CHECK_ARG(n >= 0, "%s: n_vectors must be >= 0", fn);
+  TQ_CHECK_ARG(x && codebooks && radii, "%s: null pointer", fn);
+  CsSource s{};
+  const int st = check_codebooks(codebooks, n_codebook, packed ? 16 : 256, packed ? 4 : 256, s, fn);
+  if (st != TQ_OK) return st;
+  if (packed) TQ_CHECK_ARG(p1 && p2 && p3 && p4, "%s: null output", fn);
+  else TQ_CHECK_ARG(i1 && i2 && i3 && i4, "%s: null output", fn);
+  if (n == 0) return TQ_OK;
+  Enc16Params p{};
+  p.x = x; p.P = P; p.n = n; p.D = D;
+  p.rows = std::max(1, 2048 / D);
+  p.cb = codebooks;
+  for (int l = 0; l < 4; ++l) { p.ncb[l] = s.ncb[l]; p.cb_off[l] = s.off[l]; }
+  p.i1 = i1; p.i2 = i2; p.i3 = i3; p.i4 = i4;
+  p.p1 = p1; p.p2 = p2; p.p3 = p3; p.p4 = p4;
+  p.radii = radii;
+  const int64_t grid = (n + p.rows - 1) / p.rows;
+  TQ_CHECK_ARG(grid <= (int64_t{1} << 31) - 1, "%s: too many vectors", fn);
+  const size_t shm = sizeof(float) * (1024 + 2 * static_cast<size_t>(p.rows) * D);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (packed) polar_encode16_kernel<true><<<static_cast<unsigned>(grid), 256, shm, hs>>>(p);
+  else polar_encode16_kernel<false><<<static_cast<unsigned>(grid), 256, shm, hs>>>(p);
+  TQ_CHECK_LAUNCH("polar_encode16_kernel");
+  return TQ_OK;
+}
+
+int decode16_common(const Keys16& k, const float* P, const float* codebooks, const float* cs_tables,
+                    const int* n_codebook, int64_t n, int D, int block_size, bool packed, float* out,
+                    void* stream, const char* fn) {
+  if (block_size != 16) {
+    set_error("%s: block_size must be 16 (the reference kernels hard-code it)", fn);
+    return TQ_ERR_UNSUPPORTED;
+  }
+  TQ_CHECK_ARG(D >= 16 && D <= 2048 && D % 16 == 0, "%s: dim must be a multiple of 16 in [16, 2048]", fn);
+  TQ_CHECK_ARG(n >= 0 && out && k.radii, "%s: null pointer or negative n", fn);
+  TQ_CHECK_ARG(codebooks || cs_tables, "%s: codebooks or cos/sin tables required", fn);
+  Dec16Params p{};
+  const int st = check_codebooks(codebooks, n_codebook, packed ? 16 : 256, packed ? 4 : 256, p.src, fn);
+  if (st != TQ_OK) return st;
+  p.src.cs = cs_tables;
+  p.k = k;
+  p.P = P;
+  p.out = out;
+  p.n = n;
+  p.D = D;
+  p.rows = std::max(1, 2048 / D);
+  if (n == 0) return TQ_OK;
+  const int64_t grid = (n + p.rows - 1) / p.rows;
+  const size_t shm = sizeof(float) * (2048 + static_cast<size_t>(p.rows) * D);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (packed) polar_decode16_kernel<true><<<static_cast<unsigned>(grid), 256, shm, hs>>>(p);
+  else polar_decode16_kernel<false><<<static_cast<unsigned>(grid), 256, shm, hs>>>(p);
+  TQ_CHECK_LAUNCH("polar_decode16_kernel");
+  return TQ_OK;
+}
+
+template <int D, int G, bool kPacked>
+void launch_score16(const Attn16& a, int n, int gqa, int n_sub, dim3 grid, hipStream_t s) {
+  polar16_score_kernel<D, G, kPacked><<<grid, 256, 0, s>>>(a, n, gqa, n_sub);
+}
+
+template <int D, bool kPacked>
+int dispatch_score16_g(int G, const Attn16& a, int n, int gqa, int n_sub, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: launch_score16<D, 1, kPacked>(a, n, gqa, n_sub, grid, s); break;
+    case 2: launch_score16<D, 2, kPacked>(a, n, gqa, n_sub, grid, s); break;
+    default: launch_score16<D, 4, kPacked>(a, n, gqa, n_sub, grid, s); break;
+  }
+  TQ_CHECK_LAUNCH("polar16_score_kernel");
+  return TQ_OK;
+}
+
+template <int D, bool kPacked>
+int dispatch_sdpa16_g(int G, const SdpaParams& p, const Attn16& a, dim3 grid, hipStream_t s) {
+  switch (G) {
+    case 1: polar16_sdpa_kernel<D, 1, kPacked><<<grid, 256, 0, s>>>(p, a); break;
+    case 2: polar16_sdpa_kernel<D, 2, kPacked><<<grid, 256, 0, s>>>(p, a); break;
+    default: polar16_sdpa_kernel<D, 4, kPacked><<<grid, 256, 0, s>>>(p, a); break;
+  }
+  TQ_CHECK_LAUNCH("polar16_sdpa_kernel");
+  return TQ_OK;
+}
+
+int attn16_setup(Attn16& a, const float* q, const uint8_t* i1, const uint8_t* i2, const uint8_t* i3,
+                 const uint8_t* i4, const uint32_t* p1, const uint8_t* p2, const uint8_t* p3,
+                 const uint8_t* p4, const uint16_t* radii, const float* codebooks,
+                 const int* n_codebook, bool packed, int Hq, int Hkv, int n, int D, int block_size,
+                 const char* fn) {
+  if (block_size != 16) {
+    set_error("%s: block_size must be 16 (the reference kernels hard-code it)", fn);
+    return TQ_ERR_UNSUPPORTED;
+  }
+  if (D != 64 && D != 128 && D != 256) {
+    set_error("%s: dim must be 64, 128 or 256 (got %d)", fn, D);
+    return TQ_ERR_UNSUPPORTED;
+  }
+  TQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "%s: num_heads must be a multiple of num_kv_heads", fn);
+  TQ_CHECK_ARG(n >= 0, "%s: n_keys must be >= 0", fn);
+  TQ_CHECK_ARG(q && radii && codebooks, "%s: null pointer", fn);
+  if (packed) TQ_CHECK_ARG(p1 && p2 && p3 && p4, "%s: null index array", fn);
+  else TQ_CHECK_ARG(i1 && i2 && i3 && i4, "%s: null index array", fn);
+  a = Attn16{};
+  const int st = check_codebooks(codebooks, n_codebook, packed ? 16 : 256, packed ? 4 : 256, a.src, fn);
+  if (st != TQ_OK) return st;
+  a.k.i1 = i1; a.k.i2 = i2; a.k.i3 = i3; a.k.i4 = i4;
+  a.k.p1 = p1; a.k.p2 = p2; a.k.p3 = p3; a.k.p4 = p4;
+  a.k.radii = radii;
+  a.q = q;
+  a.D = D;
+  return TQ_OK;
+}
+
+int score16_common(Attn16& a, int Hq, int Hkv, int n, float scale, float* scores, bool packed,
+                   void* stream, const char* fn) {
+  TQ_CHECK_ARG(scores != nullptr, "%s: scores is NULL", fn);
+  TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
+  if (n == 0) return TQ_OK;
+  const int gqa = Hq / Hkv, G = polar_subgroup(gqa, 4), n_sub = gqa / G;
+  a.scores = scores;
+  a.qscale = scale;
+  TQ_CHECK_ARG(Hkv * n_sub <= 65535, "%s: too many heads", fn);
+  dim3 grid((n + 1023) / 1024, Hkv * n_sub);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (a.D) {
+    case 64: return packed ? dispatch_score16_g<64, true>(G, a, n, gqa, n_sub, grid, s)
+                           : dispatch_score16_g<64, false>(G, a, n, gqa, n_sub, grid, s);
+    case 128: return packed ? dispatch_score16_g<128, true>(G, a, n, gqa, n_sub, grid, s)
+                            : dispatch_score16_g<128, false>(G, a, n, gqa, n_sub, grid, s);
+    default: return packed ? dispatch_score16_g<256, true>(G, a, n, gqa, n_sub, grid, s)
+                           : dispatch_score16_g<256, false>(G, a, n, gqa, n_sub, grid, s);
+  }
+}
+
+size_t polar_ws_size(int Hq, int Hkv, int D, int max_len, int max_g) {
+  const int gqa = Hq / Hkv, G = polar_subgroup(gqa, max_g);
+  const int64_t groups = static_cast<int64_t>(Hkv) * (gqa / G);
+  return ws_layout(1, Hq, D, polar_splits_bound(max_len, groups)).total;
+}
+
+// common split-K set-up of the polar attention kernels
+int polar_sdpa_params(SdpaParams& p, int Hq, int Hkv, int D, int n, int cap, float scale, int window,
+                      float denom_eps, int max_g, float* out, void* workspace, size_t ws_bytes,
+                      dim3& grid, int& G, const char* fn) {
+  TQ_CHECK_ARG(out != nullptr, "%s: out is NULL", fn);
+  TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
+  TQ_CHECK_ARG(window >= 0, "%s: sliding_window must be >= 0", fn);
+  TQ_CHECK_ARG(n >= 0 && cap >= 1 && n <= cap, "%s: need 0 <= kv_len <= kv_capacity", fn);
+  TQ_CHECK_ARG(Hq <= kMaxCounters, "%s: too many heads", fn);
+  const int gqa = Hq / Hkv;
+  G = polar_subgroup(gqa, max_g);
+  const int n_sub = gqa / G;
+  const int64_t groups = static_cast<int64_t>(Hkv) * n_sub;
+  const int eff = window > 0 ? std::min(n, window) : n;
+  const int chunk = polar_chunk(eff, groups);
+  const int max_splits = polar_splits_bound(eff, groups);
+  const WsLayout wl = ws_layout(1, Hq, D, max_splits);
+  if (max_splits > 1 && (!workspace || ws_bytes < wl.total)) {
+    set_error("%s: workspace of %zu bytes needed (got %zu)", fn, wl.total, ws_bytes);
+    return TQ_ERR_WORKSPACE;
+  }
+  TQ_CHECK_ARG(Hkv * n_sub <= 65535, "%s: too many heads", fn);
+  p = SdpaParams{};
+  p.out = out;
+  char* ws = static_cast<char*>(workspace);
+  p.ws_cnt = ws ? reinterpret_cast<int*>(ws + wl.cnt_off) : nullptr;
+  p.ws_ml = ws ? reinterpret_cast<float*>(ws + wl.ml_off) : nullptr;
+  p.ws_o = ws ? reinterpret_cast<float*>(ws + wl.o_off) : nullptr;
+  p.Hq = Hq; p.Hkv = Hkv; p.cap = cap; p.gqa = gqa; p.n_sub = n_sub;
+  p.n = n; p.n_clamp = n; p.window = window;
+  p.scale_log2 = scale * kLog2e;
+  p.chunk = chunk;
+  p.max_splits = max_splits;
+  p.denom_eps = denom_eps;
+  grid = dim3(max_splits, Hkv * n_sub, 1);
+  return TQ_OK;
+}
+
+int p7_keys_setup(P7Keys& k, const float* qp, const float* qs, const uint32_t* angles,
+                  const uint32_t* norms, const uint32_t* qjl, const float* cs_tables, int Hq,
+                  int Hkv, const char* fn) {
+  TQ_CHECK_ARG(qp && qs && angles && norms && qjl && cs_tables, "%s: null pointer", fn);
+  TQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "%s: num_heads must be a multiple of num_kv_heads", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(angles) % 16 == 0 && reinterpret_cast<uintptr_t>(qjl) % 16 == 0,
+               "%s: angles / qjl must be 16-byte aligned", fn);
+  k = P7Keys{};
+  k.qp = qp; k.qs = qs; k.cs = cs_tables;
+  k.angles = angles; k.norms = norms; k.qjl = qjl;
+  return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tq_polar_quantize(const float* x, const float* precondition, const float* codebooks,
+                      const int* n_codebook, int64_t n_vectors, int dim, int block_size,
+                      uint8_t* idx_l1, uint8_t* idx_l2, uint8_t* idx_l3, uint8_t* idx_l4,
+                      uint16_t* radii, void* stream) {
+  return encode16_common(x, precondition, codebooks, n_codebook, n_vectors, dim, block_size, false,
+                         idx_l1, idx_l2, idx_l3, idx_l4, nullptr, nullptr, nullptr, nullptr, radii,
+                         stream, "tq_polar_quantize");
+}
+
+int tq_polar_quantize_packed(const float* x, const float* precondition, const float* codebooks,
+                             const int* n_codebook, int64_t n_vectors, int dim, int block_size,
+                             uint32_t* packed_l1, uint8_t* packed_l2, uint8_t* packed_l3,
+                             uint8_t* packed_l4, uint16_t* radii, void* stream) {
+  return encode16_common(x, precondition, codebooks, n_codebook, n_vectors, dim, block_size, true,
+                         nullptr, nullptr, nullptr, nullptr, packed_l1, packed_l2, packed_l3,
+                         packed_l4, radii, stream, "tq_polar_quantize_packed");
+}
+
+int tq_polar_dequantize(const uint8_t* idx_l1, const uint8_t* idx_l2, const uint8_t* idx_l3,
+                        const uint8_t* idx_l4, const uint16_t* radii, const float* precondition,
+                        const float* codebooks, const int* n_codebook, int64_t n_vectors, int dim,
+                        int block_size, float* out, void* stream) {
+  Keys16 k{};
+  k.i1 = idx_l1; k.i2 = idx_l2; k.i3 = idx_l3; k.i4 = idx_l4; k.radii = radii;
+  TQ_CHECK_ARG(idx_l1 && idx_l2 && idx_l3 && idx_l4, "tq_polar_dequantize: null index array");
+  return decode16_common(k, precondition, codebooks, nullptr, n_codebook, n_vectors, dim, block_size,
+                         false, out, stream, "tq_polar_dequantize");
+}
+
+int tq_polar_dequantize_packed(const uint32_t* packed_l1, const uint8_t* packed_l2,
+                               const uint8_t* packed_l3, const uint8_t* packed_l4,
+                               const uint16_t* radii, const float* codebooks,
+                               const float* cs_tables, const int* n_codebook, int64_t n_vectors,
+                               int dim, int block_size, float* out, void* stream) {
+  Keys16 k{};
+  k.p1 = packed_l1; k.p2 = packed_l2; k.p3 = packed_l3; k.p4 = packed_l4; k.radii = radii;
+  TQ_CHECK_ARG(packed_l1 && packed_l2 && packed_l3 && packed_l4,
+               "tq_polar_dequantize_packed: null index array");
+  return decode16_common(k, nullptr, codebooks, cs_tables, n_codebook, n_vectors, dim, block_size,
+                         true, out, stream, "tq_polar_dequantize_packed");
+}
+
+int tq_compressed_score(const float* q, int num_heads, const uint8_t* idx_l1, const uint8_t* idx_l2,
+                        const uint8_t* idx_l3, const uint8_t* idx_l4, const uint16_t* radii,
+                        const float* codebooks, const int* n_codebook, int num_kv_heads,
+                        int n_keys, int dim, int block_size, float scale, float* scores,
+                        void* stream) {
+  const char* fn = "tq_compressed_score";
+  Attn16 a;
+  int st = attn16_setup(a, q, idx_l1, idx_l2, idx_l3, idx_l4, nullptr, nullptr, nullptr, nullptr,
+                        radii, codebooks, n_codebook, false, num_heads, num_kv_heads, n_keys, dim,
+                        block_size, fn);
+  if (st != TQ_OK) return st;
+  return score16_common(a, num_heads, num_kv_heads, n_keys, scale, scores, false, stream, fn);
+}
+
+int tq_compressed_score_packed(const float* q, int num_heads, const uint32_t* packed_l1,
+                               const uint8_t* packed_l2, const uint8_t* packed_l3,
+                               const uint8_t* packed_l4, const uint16_t* radii,
+                               const float* codebooks, const int* n_codebook, int num_kv_heads,
+                               int n_keys, int dim, int block_size, float scale, float* scores,
+                               void* stream) {
+  const char* fn = "tq_compressed_score_packed";
+  Attn16 a;
+  int st = attn16_setup(a, q, nullptr, nullptr, nullptr, nullptr, packed_l1, packed_l2, packed_l3,
+                        packed_l4, radii, codebooks, n_codebook, true, num_heads, num_kv_heads,
+                        n_keys, dim, block_size, fn);
+  if (st != TQ_OK) return st;
+  return score16_common(a, num_heads, num_kv_heads, n_keys, scale, scores, true, stream, fn);
+}
+
+size_t tq_compressed_sdpa_workspace_size(int num_heads, int num_kv_heads, int dim, int max_n_keys) {
+  if (num_kv_heads < 1 || num_heads < num_kv_heads || max_n_keys < 0 || dim < 1) return 0;
+  return polar_ws_size(num_heads, num_kv_heads, dim, max_n_keys, 4);
+}
+
+int tq_compressed_sdpa(const float* q, int num_heads, const uint8_t* idx_l1, const uint8_t* idx_l2,
+                       const uint8_t* idx_l3, const uint8_t* idx_l4, const uint16_t* radii,
+                       const float* codebooks, const int* n_codebook, const float* values,
+                       int num_kv_heads, int n_keys, int dim, int block_size, float scale,
+                       float* out, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "tq_compressed_sdpa";
+  Attn16 a;
+  int st = attn16_setup(a, q, idx_l1, idx_l2, idx_l3, idx_l4, nullptr, nullptr, nullptr, nullptr,
+                        radii, codebooks, n_codebook, false, num_heads, num_kv_heads, n_keys, dim,
+                        block_size, fn);
+  if (st != TQ_OK) return st;
+  TQ_CHECK_ARG(values != nullptr, "%s: values is NULL", fn);
+  SdpaParams p;
+  dim3 grid;
+  int G = 1;
+  st = polar_sdpa_params(p, num_heads, num_kv_heads, dim, n_keys, std::max(n_keys, 1), scale, 0,
+                         1e-8f, 4, out, workspace, workspace_bytes, grid, G, fn);
+  if (st != TQ_OK) return st;
+  a.values = values;
+  a.qscale = scale * kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dim) {
+    case 64: return dispatch_sdpa16_g<64, false>(G, p, a, grid, s);
+    case 128: return dispatch_sdpa16_g<128, false>(G, p, a, grid, s);
+    default: return dispatch_sdpa16_g<256, false>(G, p, a, grid, s);
+  }
+}
+
+int tq_polar_rotate(const float* x, const float* precondition, int64_t rows, int dim, float* y,
+                    void* stream) {
+  TQ_CHECK_ARG(x && precondition && y, "tq_polar_rotate: null pointer");
+  if (dim != 128) {
+    set_error("tq_polar_rotate: dim must be 128 (got %d)", dim);
+    return TQ_ERR_UNSUPPORTED;
+  }
+  TQ_CHECK_ARG(rows >= 0 && rows <= 0x7FFFFFFF, "tq_polar_rotate: bad rows");
+  if (rows == 0) return TQ_OK;
+  rotate128_kernel<<<static_cast<unsigned>(rows), 128, 0, static_cast<hipStream_t>(stream)>>>(
+      x, precondition, y, static_cast<int>(rows));
+  TQ_CHECK_LAUNCH("rotate128_kernel");
+  return TQ_OK;
+}
+
+int tq_qjl_query(const float* q_rot, const float* sketch, int num_heads, float* q_sketch,
+                 void* stream) {
+  // S q' per head: the same product as the rotation with S in place of P
+  TQ_CHECK_ARG(q_rot && sketch && q_sketch && num_heads >= 0, "tq_qjl_query: bad argument");
+  if (num_heads == 0) return TQ_OK;
+  rotate128_kernel<<<num_heads, 128, 0, static_cast<hipStream_t>(stream)>>>(q_rot, sketch, q_sketch,
+                                                                             num_heads);
+  TQ_CHECK_LAUNCH("rotate128_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_encode(const float* x, const float* precondition, const float* sketch,
+                     const float* codebooks, const float* cs_tables, int64_t n_vectors,
+                     uint32_t* angles, uint32_t* norms, uint32_t* qjl, void* stream) {
+  const char* fn = "tq_polar7_encode";
+  TQ_CHECK_ARG(x && sketch && codebooks && cs_tables && angles && norms && qjl, "%s: null pointer", fn);
+  TQ_CHECK_ARG(n_vectors >= 0, "%s: n_vectors must be >= 0", fn);
+  if (n_vectors == 0) return TQ_OK;
+  P7EncParams p{};
+  p.x = x; p.P = precondition; p.S = sketch; p.cb = codebooks; p.cs = cs_tables;
+  p.n = n_vectors;
+  p.angles = angles; p.norms = norms; p.qjl = qjl;
+  const int64_t grid = std::min<int64_t>((n_vectors + 3) / 4, 8192);
+  polar7_encode_kernel<<<static_cast<unsigned>(grid), 256, 0, static_cast<hipStream_t>(stream)>>>(p);
+  TQ_CHECK_LAUNCH("polar7_encode_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_kv_append(const float* k_new, const float* precondition, const float* sketch,
+                        const float* codebooks, const float* cs_tables, uint32_t* angles,
+                        uint32_t* norms, uint32_t* qjl, int batch, int num_kv_heads,
+                        int kv_capacity, const int32_t* positions, int n_new, void* stream) {
+  const char* fn = "tq_polar7_kv_append";
+  TQ_CHECK_ARG(k_new && sketch && codebooks && cs_tables && angles && norms && qjl && positions,
+               "%s: null pointer", fn);
+  TQ_CHECK_ARG(batch >= 1 && num_kv_heads >= 1 && kv_capacity >= 1 && n_new >= 0,
+               "%s: bad shape", fn);
+  if (n_new == 0) return TQ_OK;
+  P7EncParams p{};
+  p.x = k_new; p.P = precondition; p.S = sketch; p.cb = codebooks; p.cs = cs_tables;
+  p.n = static_cast<int64_t>(batch) * num_kv_heads * n_new;
+  p.positions = positions; p.n_new = n_new; p.cap = kv_capacity; p.Hkv = num_kv_heads;
+  p.angles = angles; p.norms = norms; p.qjl = qjl;
+  const int64_t grid = std::min<int64_t>((p.n + 3) / 4, 8192);
+  polar7_encode_kernel<<<static_cast<unsigned>(grid), 256, 0, static_cast<hipStream_t>(stream)>>>(p);
+  TQ_CHECK_LAUNCH("polar7_encode_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_score(const float* q_rot, const float* q_sketch, const uint32_t* angles,
+                    const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
+                    int num_heads, int num_kv_heads, int kv_len, int kv_capacity, float scale,
+                    float* scores, void* stream) {
+  const char* fn = "tq_polar7_score";
+  P7Keys k;
+  int st = p7_keys_setup(k, q_rot, q_sketch, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
+  if (st != TQ_OK) return st;
+  TQ_CHECK_ARG(scores != nullptr, "%s: scores is NULL", fn);
+  TQ_CHECK_ARG(kv_len >= 0 && kv_capacity >= 1 && kv_len <= kv_capacity, "%s: bad kv_len", fn);
+  TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
+  if (kv_len == 0) return TQ_OK;
+  k.scores = scores;
+  const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, 4), n_sub = gqa / G;
+  TQ_CHECK_ARG(num_kv_heads * n_sub <= 65535, "%s: too many heads", fn);
+  dim3 grid((kv_len + 1023) / 1024, num_kv_heads * n_sub);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (G) {
+    case 1: polar7_score_kernel<1><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale); break;
+    case 2: polar7_score_kernel<2><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale); break;
+    default: polar7_score_kernel<4><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale); break;
+  }
+  TQ_CHECK_LAUNCH("polar7_score_kernel");
+  return TQ_OK;
+}
+
+size_t tq_polar7_sdpa_workspace_size(int num_heads, int num_kv_heads, int max_kv_len) {
+  if (num_kv_heads < 1 || num_heads < num_kv_heads || max_kv_len < 0) return 0;
+  return polar_ws_size(num_heads, num_kv_heads, 128, max_kv_len, 4);
+}
+
+int tq_polar7_sdpa_int4v(const float* q_rot, const float* q_sketch, const uint32_t* angles,
+                         const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
+                         const uint32_t* v_quant, const void* v_scales, const void* v_biases,
+                         tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
+                         int kv_len, int kv_capacity, float scale, int sliding_window,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "tq_polar7_sdpa_int4v";
+  P7Keys k;
+  int st = p7_keys_setup(k, q_rot, q_sketch, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
+  if (st != TQ_OK) return st;
+  TQ_CHECK_ARG(v_quant && v_scales && v_biases, "%s: null V pointer", fn);
+  TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32, "%s: sb_dtype must be f16 or f32", fn);
+  SdpaParams p;
+  dim3 grid;
+  int G = 1;
+  st = polar_sdpa_params(p, num_heads, num_kv_heads, 128, kv_len, kv_capacity, scale, sliding_window,
+                         0.0f, 4, out, workspace, workspace_bytes, grid, G, fn);
+  if (st != TQ_OK) return st;
+  p.vq = v_quant; p.vs = v_scales; p.vb = v_biases;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = sb_dtype == TQ_F16;
+  if (f16) {
+    if (G == 1) polar7_sdpa_kernel<1, __half><<<grid, 256, 0, s>>>(p, k);
+    else if (G == 2) polar7_sdpa_kernel<2, __half><<<grid, 256, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<4, __half><<<grid, 256, 0, s>>>(p, k);
+  } else {
+    if (G == 1) polar7_sdpa_kernel<1, float><<<grid, 256, 0, s>>>(p, k);
+    else if (G == 2) polar7_sdpa_kernel<2, float><<<grid, 256, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<4, float><<<grid, 256, 0, s>>>(p, k);
+  }
+  TQ_CHECK_LAUNCH("polar7_sdpa_kernel");
+  return TQ_OK;
+}
+
+}  // extern "C"

@@ -38,6 +38,78 @@
 #include "tq_sdpa_common.h"
 
 namespace tq {
+
+// ---- split planning and workspace layout (shared with tq_polar.hip) ----------
+
+// Workgroups per launch the split planner aims for: one per CU (the matrix
+// kernel runs one 4-wave workgroup per CU at its register budget; more,
+// smaller splits only add per-split fixed cost).  Queried once per process
+// from the current device.
+int target_wgs() {
+  static int cached = [] {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    return cus;
+  }();
+  return cached;
+}
+namespace {
+constexpr int kMinChunk = 128;
+constexpr int kChunkGranule = 128;
+}  // namespace
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : dflt;
+}
+
+int head_subgroup(int gqa) {
+  for (int g : {8, 4, 2}) if (gqa % g == 0) return g;
+  return 1;
+}
+
+// Keys per workgroup: enough workgroups to fill 256 CUs several times over,
+// never fewer than kMinChunk rows.
+int plan_chunk(int max_len, int64_t groups) {
+  // never more than kMaxSplits chunks per sequence
+  const int64_t floor_c = (static_cast<int64_t>(max_len) + kMaxSplits - 1) / kMaxSplits;
+  const int forced = env_int("TQ_SDPA_CHUNK", 0);
+  if (forced > 0) return static_cast<int>(std::max<int64_t>(forced, floor_c));
+  const int64_t want = (static_cast<int64_t>(max_len) * groups + target_wgs() - 1) / target_wgs();
+  int64_t c = (want + kChunkGranule - 1) / kChunkGranule * kChunkGranule;
+  c = std::max<int64_t>({c, int64_t{kMinChunk}, floor_c});
+  return static_cast<int>(std::min<int64_t>(c, 1 << 30));
+}
+
+// Upper bound of ceil(L / plan_chunk(L, groups)) over every L <= max_len
+// (plan_chunk is not monotone in L, the bound is): sizes grids and workspaces.
+int max_splits_bound(int max_len, int64_t groups) {
+  if (max_len <= 0) return 1;
+  const int forced = env_int("TQ_SDPA_CHUNK", 0);
+  if (forced > 0) return std::min((max_len + forced - 1) / forced, kMaxSplits);  // chunk >= ceil(L/kMaxSplits)
+  const int64_t by_len = (static_cast<int64_t>(max_len) + kMinChunk - 1) / kMinChunk;
+  const int64_t by_wgs = (target_wgs() + groups - 1) / groups;
+  return static_cast<int>(std::max<int64_t>(1, std::min({by_len, by_wgs, int64_t{kMaxSplits}})));
+}
+
+// Workspace: [split counters | (m, l) partials | O partials].  The counter
+// region has a FIXED size at offset 0 so that no call's partials ever overlap
+// another call's counters: counters must read zero on entry (the kernels
+// return every counter they use to zero), whatever shapes earlier calls had.
+WsLayout ws_layout(int batch, int Hq, int D, int max_splits) {
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  WsLayout w;
+  w.cnt_off = 0;
+  w.ml_off = sizeof(int) * static_cast<size_t>(kMaxCounters);
+  w.o_off = w.ml_off + up(sizeof(float) * 2 * static_cast<size_t>(batch) * Hq * max_splits);
+  w.total = w.o_off + up(sizeof(float) * static_cast<size_t>(batch) * Hq * max_splits * D);
+  return w;
+}
+
+
 namespace {
 
 constexpr int kPrefetch = 4;  // row steps in flight per wave
@@ -270,78 +342,6 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
 }
 
 // ---- host side ---------------------------------------------------------------
-
-// Workgroups per launch the split planner aims for: one per CU (the matrix
-// kernel runs one 4-wave workgroup per CU at its register budget; more,
-// smaller splits only add per-split fixed cost).  Queried once per process
-// from the current device.
-int target_wgs() {
-  static int cached = [] {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    return cus;
-  }();
-  return cached;
-}
-constexpr int kMinChunk = 128;
-constexpr int kChunkGranule = 128;
-
-int env_int(const char* name, int dflt) {
-  const char* v = std::getenv(name);
-  return v ? std::atoi(v) : dflt;
-}
-
-int head_subgroup(int gqa) {
-  for (int g : {8, 4, 2}) if (gqa % g == 0) return g;
-  return 1;
-}
-
-// Keys per workgroup: enough workgroups to fill 256 CUs several times over,
-// never fewer than kMinChunk rows.
-int plan_chunk(int max_len, int64_t groups) {
-  // never more than kMaxSplits chunks per sequence
-  const int64_t floor_c = (static_cast<int64_t>(max_len) + kMaxSplits - 1) / kMaxSplits;
-  const int forced = env_int("TQ_SDPA_CHUNK", 0);
-  if (forced > 0) return static_cast<int>(std::max<int64_t>(forced, floor_c));
-  const int64_t want = (static_cast<int64_t>(max_len) * groups + target_wgs() - 1) / target_wgs();
-  int64_t c = (want + kChunkGranule - 1) / kChunkGranule * kChunkGranule;
-  c = std::max<int64_t>({c, int64_t{kMinChunk}, floor_c});
-  return static_cast<int>(std::min<int64_t>(c, 1 << 30));
-}
-
-// Upper bound of ceil(L / plan_chunk(L, groups)) over every L <= max_len
-// (plan_chunk is not monotone in L, the bound is): sizes grids and workspaces.
-int max_splits_bound(int max_len, int64_t groups) {
-  if (max_len <= 0) return 1;
-  const int forced = env_int("TQ_SDPA_CHUNK", 0);
-  if (forced > 0) return std::min((max_len + forced - 1) / forced, kMaxSplits);  // chunk >= ceil(L/kMaxSplits)
-  const int64_t by_len = (static_cast<int64_t>(max_len) + kMinChunk - 1) / kMinChunk;
-  const int64_t by_wgs = (target_wgs() + groups - 1) / groups;
-  return static_cast<int>(std::max<int64_t>(1, std::min({by_len, by_wgs, int64_t{kMaxSplits}})));
-}
-
-// Workspace: [split counters | (m, l) partials | O partials].  The counter
-// region has a FIXED size at offset 0 so that no call's partials ever overlap
-// another call's counters: counters must read zero on entry (the kernels
-// return every counter they use to zero), whatever shapes earlier calls had.
-constexpr int64_t kMaxCounters = 1 << 16;  // batch * num_heads
-
-struct WsLayout {
-  size_t cnt_off, ml_off, o_off, total;
-};
-
-WsLayout ws_layout(int batch, int Hq, int D, int max_splits) {
-  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
-  WsLayout w;
-  w.cnt_off = 0;
-  w.ml_off = sizeof(int) * static_cast<size_t>(kMaxCounters);
-  w.o_off = w.ml_off + up(sizeof(float) * 2 * static_cast<size_t>(batch) * Hq * max_splits);
-  w.total = w.o_off + up(sizeof(float) * static_cast<size_t>(batch) * Hq * max_splits * D);
-  return w;
-}
 
 template <int D, int G>
 int launch_dg(const SdpaParams& p, int sb_dtype, dim3 grid, hipStream_t s) {

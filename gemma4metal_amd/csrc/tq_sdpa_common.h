@@ -37,6 +37,10 @@ struct SdpaParams {
   float scale_log2;        // scale * log2(e)
   int chunk;
   int max_splits;
+  // Output normalisation: 0 -> out = l > 0 ? O / l : 0 (sdpa_int4,
+  // lib/turboquant.metal:886); > 0 -> out = O / (l + denom_eps)
+  // (sdpa_tq_sequential, lib/turboquant.metal:222).
+  float denom_eps;
 };
 
 // The keys one workgroup attends: rows [t_begin, t_end) of its sequence's
@@ -108,6 +112,10 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ float normalise(float O, float L, float eps) {
+  return eps > 0.0f ? O / (L + eps) : (L > 0.0f ? O / L : 0.0f);
+}
+
 __device__ __forceinline__ float merge_factor(float m, float M) {
   return m == -INFINITY ? 0.0f : fast_exp2(m - M);
 }
@@ -146,7 +154,7 @@ struct Finalize {
         Ls += l(arena, w)[h] * f;
       }
       if (S == 1) {
-        p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+        p.out[(head_base + h) * D + d] = normalise(O, Ls, p.denom_eps);
       } else {
         const int64_t slot = (head_base + h) * p.max_splits + split;
         store_coherent(p.ws_o + slot * D + d, O);
@@ -204,10 +212,28 @@ struct Finalize {
         O = fmaf(load_coherent(po + static_cast<int64_t>(sp) * D), f, O);
         Ls = fmaf(ls[sp], f, Ls);
       }
-      p.out[(head_base + h) * D + d] = Ls > 0.0f ? O / Ls : 0.0f;
+      p.out[(head_base + h) * D + d] = normalise(O, Ls, p.denom_eps);
     }
   }
 };
+
+// ---- host-side split planning (tq_sdpa.hip) ---------------------------------
+// Workspace: [split counters | (m, l) partials | O partials].  The counter
+// region has a FIXED size at offset 0 so that no call's partials ever overlap
+// another call's counters: counters must read zero on entry (the kernels
+// return every counter they use to zero), whatever shapes earlier calls had.
+constexpr int64_t kMaxCounters = 1 << 16;  // batch * num_heads
+
+struct WsLayout {
+  size_t cnt_off, ml_off, o_off, total;
+};
+
+int target_wgs();                                   // CUs of the current device
+int env_int(const char* name, int dflt);
+int head_subgroup(int gqa);                         // query heads per workgroup
+int plan_chunk(int max_len, int64_t groups);        // keys per workgroup
+int max_splits_bound(int max_len, int64_t groups);  // bound of ceil(L / chunk)
+WsLayout ws_layout(int batch, int Hq, int D, int max_splits);
 
 // Launch of the matrix-core kernel (tq_sdpa_mfma.hip).  Returns TQ_OK,
 // a tq_status error, or -1 when (D, G) is not served by that kernel.

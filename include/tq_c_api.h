@@ -130,6 +130,140 @@ int tq_kv_append_int4(const void* k_new, const void* v_new, tq_dtype x_dtype,
 int tq_dequantize_int4(const uint32_t* w_q, const void* scales, const void* biases,
                        tq_dtype sb_dtype, int64_t rows, int dim, float* out, void* stream);
 
+/* ---- PolarQuant, reference layouts (16-value blocks, 4 levels) -------------
+ * Codebooks: `codebooks` is a DEVICE float array holding the level 1..4
+ * codebooks back to back (angles, radians); `n_codebook` a HOST int[4] with
+ * their sizes.  Level 1 angles are atan2 wrapped to [0, 2pi), levels 2-4 are
+ * in [0, pi/2]; each angle becomes the index of the nearest entry under
+ * |theta - c| (first minimum wins, lib/turboquant.metal:38-42).  Sizes: <= 256
+ * per level unpacked; <= 16 (level 1) and <= 4 (levels 2-4) packed.
+ * Blocks are the n_vectors * dim / 16 consecutive 16-value slices of the
+ * (rotated) vectors, in row-major order.  block_size must be 16 (the
+ * reference kernels hard-code it, lib/turboquant.metal:25-27). */
+
+/* Replaces turboquant::polar_quantize (lib/turboquant.h:52-60,
+ * lib/turboquant.cpp:97-110; kernel lib/turboquant.metal:8-98).  x [n, dim]
+ * f32; precondition [dim, dim] f32 (y = x P^T) or NULL when x is already
+ * rotated.  Outputs idx_l1 u8 [nb*8], idx_l2 [nb*4], idx_l3 [nb*2],
+ * idx_l4 [nb], radii f16 bits [nb]. */
+int tq_polar_quantize(const float* x, const float* precondition, const float* codebooks,
+                      const int* n_codebook, int64_t n_vectors, int dim, int block_size,
+                      uint8_t* idx_l1, uint8_t* idx_l2, uint8_t* idx_l3, uint8_t* idx_l4,
+                      uint16_t* radii, void* stream);
+
+/* Replaces turboquant::polar_quantize_packed (lib/turboquant.h:77-82,
+ * lib/turboquant.cpp:255-272; kernel lib/turboquant.metal:501-600): per
+ * block one u32 (level-1 index j at bits 4j), one u8 each for levels 2, 3, 4
+ * (index j at bits 2j), one f16 radius. */
+int tq_polar_quantize_packed(const float* x, const float* precondition, const float* codebooks,
+                             const int* n_codebook, int64_t n_vectors, int dim, int block_size,
+                             uint32_t* packed_l1, uint8_t* packed_l2, uint8_t* packed_l3,
+                             uint8_t* packed_l4, uint16_t* radii, void* stream);
+
+/* Replaces turboquant::polar_dequantize (precondition != NULL: x = y P,
+ * lib/turboquant.cpp:112-123) and polar_dequantize_fast (precondition ==
+ * NULL: y only, lib/turboquant.cpp:191-200); kernel
+ * lib/turboquant.metal:100-164.  out [n_vectors, dim] f32. */
+int tq_polar_dequantize(const uint8_t* idx_l1, const uint8_t* idx_l2, const uint8_t* idx_l3,
+                        const uint8_t* idx_l4, const uint16_t* radii, const float* precondition,
+                        const float* codebooks, const int* n_codebook, int64_t n_vectors, int dim,
+                        int block_size, float* out, void* stream);
+
+/* Replaces polar_dequantize_packed (cs_tables == NULL: cos/sin of the
+ * codebook angles, lib/turboquant.cpp:274-282, kernel
+ * lib/turboquant.metal:602-653) and polar_dequantize_packed_fast (cs_tables =
+ * DEVICE float (cos, sin) pairs laid out like the codebooks,
+ * lib/turboquant.cpp:312-320, kernel :655-704).  Output y (no
+ * preconditioner), as the reference. */
+int tq_polar_dequantize_packed(const uint32_t* packed_l1, const uint8_t* packed_l2,
+                               const uint8_t* packed_l3, const uint8_t* packed_l4,
+                               const uint16_t* radii, const float* codebooks,
+                               const float* cs_tables, const int* n_codebook, int64_t n_vectors,
+                               int dim, int block_size, float* out, void* stream);
+
+/* Replaces turboquant::compressed_score (lib/turboquant.h:157-165,
+ * lib/turboquant.cpp:323-359; kernel tq_score_shared,
+ * lib/turboquant.metal:424-499): scores[h, n] = sum_d scale q[h, d]
+ * khat[(h / gqa) * n_keys + n, d] for q [num_heads, dim] f32 (preconditioned),
+ * keys of num_kv_heads heads x n_keys; gqa = num_heads / num_kv_heads (the
+ * reference is gqa = 1).  dim in {64, 128, 256}. scores [num_heads, n_keys]. */
+int tq_compressed_score(const float* q, int num_heads, const uint8_t* idx_l1, const uint8_t* idx_l2,
+                        const uint8_t* idx_l3, const uint8_t* idx_l4, const uint16_t* radii,
+                        const float* codebooks, const int* n_codebook, int num_kv_heads,
+                        int n_keys, int dim, int block_size, float scale, float* scores,
+                        void* stream);
+/* The same over the packed layout (no reference counterpart: the reference
+ * scores only unpacked keys). */
+int tq_compressed_score_packed(const float* q, int num_heads, const uint32_t* packed_l1,
+                               const uint8_t* packed_l2, const uint8_t* packed_l3,
+                               const uint8_t* packed_l4, const uint16_t* radii,
+                               const float* codebooks, const int* n_codebook, int num_kv_heads,
+                               int n_keys, int dim, int block_size, float scale, float* scores,
+                               void* stream);
+
+/* Replaces turboquant::compressed_sdpa (lib/turboquant.h:127-143,
+ * lib/turboquant.cpp:125-188; kernel sdpa_tq_sequential,
+ * lib/turboquant.metal:166-224): out[h] = sum_n softmax(scores[h])_n
+ * values[(h / gqa) * n_keys + n] / (l + 1e-8) semantics of :222, values
+ * [num_kv_heads * n_keys, dim] f32.  Split-K: workspace as tq_sdpa_int4
+ * (zero-filled once, its first 256 KiB are counters that calls return to
+ * zero). */
+size_t tq_compressed_sdpa_workspace_size(int num_heads, int num_kv_heads, int dim, int max_n_keys);
+int tq_compressed_sdpa(const float* q, int num_heads, const uint8_t* idx_l1, const uint8_t* idx_l2,
+                       const uint8_t* idx_l3, const uint8_t* idx_l4, const uint16_t* radii,
+                       const float* codebooks, const int* n_codebook, const float* values,
+                       int num_kv_heads, int n_keys, int dim, int block_size, float scale,
+                       float* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- 7-level PolarQuant + QJL (D = 128) ----------------
+ * No reference kernel: the same polar recursion as polar_quantize over one
+ * 128-value block (7 levels; level-1 angles 4-bit, levels 2-7 2-bit) plus
+ * the QJL residual sketch the reference README describes (README.md:11,176).
+ * Per vector (row of a [.., capacity, .] cache):
+ *   angles u32 [12]: words 0-7 level 1 (pair j at word j/8, bits 4(j%8)),
+ *     words 8-9 level 2 (pair j at word 8 + j/16, bits 2(j%16)), word 10
+ *     level 3 (bits 2j), word 11 levels 4 (bits 2j), 5 (16+2j), 6 (24+2j),
+ *     7 (28-29);
+ *   norms u32: fp16 radius (bits 0-15) | fp16 ||r|| (bits 16-31);
+ *   qjl u32 [4]: bit i of word i/32 = [(S r)_i >= 0], r = y - yhat.
+ * codebooks: DEVICE float[20] = level-1 codebook [16] then the levels 2-7
+ * codebook [4]; cs_tables: DEVICE float[40] = their (cos, sin) pairs (the
+ * decoder's tables; the encoder's residual uses the same values).
+ * sketch: DEVICE S [128][128] f32. */
+int tq_polar7_encode(const float* x, const float* precondition, const float* sketch,
+                     const float* codebooks, const float* cs_tables, int64_t n_vectors,
+                     uint32_t* angles, uint32_t* norms, uint32_t* qjl, void* stream);
+/* Encode k_new [batch, num_kv_heads, n_new, 128] f32 into rows
+ * positions[b] .. positions[b] + n_new - 1 of the [batch, num_kv_heads,
+ * kv_capacity, .] caches (rows outside [0, kv_capacity) are not written). */
+int tq_polar7_kv_append(const float* k_new, const float* precondition, const float* sketch,
+                        const float* codebooks, const float* cs_tables, uint32_t* angles,
+                        uint32_t* norms, uint32_t* qjl, int batch, int num_kv_heads,
+                        int kv_capacity, const int32_t* positions, int n_new, void* stream);
+/* y = x P^T for rows of 128 (the query rotation q' = P q), and the query
+ * sketch S q'. */
+int tq_polar_rotate(const float* x, const float* precondition, int64_t rows, int dim, float* y,
+                    void* stream);
+int tq_qjl_query(const float* q_rot, const float* sketch, int num_heads, float* q_sketch,
+                 void* stream);
+/* scores[h, n] = scale * (<q'_h, yhat_n> + sqrt(pi/2)/128 * ||r_n|| *
+ * <S q'_h, sign(S r_n)>) over rows [0, kv_len) of kv head h / gqa. */
+int tq_polar7_score(const float* q_rot, const float* q_sketch, const uint32_t* angles,
+                    const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
+                    int num_heads, int num_kv_heads, int kv_len, int kv_capacity, float scale,
+                    float* scores, void* stream);
+/* Decode attention over those scores (window rule and empty-set rule of
+ * tq_sdpa_int4) with int4 V [num_kv_heads, kv_capacity, 16] + scale/bias
+ * [.., 2] in sb_dtype; out [num_heads, 128] f32.  Workspace as
+ * tq_sdpa_int4. */
+size_t tq_polar7_sdpa_workspace_size(int num_heads, int num_kv_heads, int max_kv_len);
+int tq_polar7_sdpa_int4v(const float* q_rot, const float* q_sketch, const uint32_t* angles,
+                         const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
+                         const uint32_t* v_quant, const void* v_scales, const void* v_biases,
+                         tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
+                         int kv_len, int kv_capacity, float scale, int sliding_window,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
