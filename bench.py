@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8, help="distinct KV sets rotated")
     ap.add_argument("--workload", default="ctx32k",
-                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream"])
+                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar"])
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -232,6 +232,10 @@ def main():
                          "parallelism": "none (1 GPU)"}}, args)
         return
 
+    if args.workload == "polar":
+        bench_polar(args, torch, gen)
+        return
+
     if args.workload == "sliding50":
         L, W, layers = 786, 1024, 50
         sets = [gen_cache(tq, torch, Hkv, L, D, gen) for _ in range(layers)]
@@ -301,6 +305,72 @@ def main():
                          "global_batch": B, "seq_len": cap, "parallelism": "none (1 GPU)",
                          "algorithmic_bytes": nbytes}}, args)
         return
+
+
+def bench_polar(args, torch, gen):
+    """PolarQuant (7 levels) + QJL keys and int4 V at
+    Hq=32, Hkv=16, D=128, L=32768, N(0,1) keys and query, attn_scale 1.0.
+    A step = query preparation (q' = P q, S q') + the fused attention
+    launch; the score-only launch is timed beside it."""
+    from gemma4metal_amd import polar as pq
+    from gemma4metal_amd import turboquant as tq
+    from oracle import polar as PQ
+    Hq, Hkv, D, L = 32, 16, 128, 32768
+    P = torch.linalg.qr(torch.randn((D, D), generator=gen, device="cuda", dtype=torch.float64))[0]
+    P = P.to(torch.float32).contiguous()
+    S = torch.randn((128, D), generator=gen, device="cuda")
+    codec = pq.Polar7Codec(P, S)
+    nsets = args.sets
+    sets = []
+    for _ in range(nsets):
+        k = torch.randn((Hkv, L, D), generator=gen, device="cuda")
+        v = torch.randn((Hkv, L, D), generator=gen, device="cuda")
+        keys = codec.encode(k)
+        vals = tq.quantize(v, scale_dtype=torch.float16)
+        sets.append((keys, vals))
+        del k, v
+    qs_ = [torch.randn((Hq, D), generator=gen, device="cuda") for _ in range(nsets)]
+    out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
+    nbytes = PQ.polar7_decode_bytes(Hq, Hkv, L)
+    prepared = [codec.prepare_query(q) for q in qs_]
+
+    def step(i):
+        s = i % nsets
+        tab = codec.prepare_query(qs_[s])
+        codec.sdpa_int4v(tab, *sets[s][0], *sets[s][1], 1.0, 0, out=out)
+
+    def attn_only(i):
+        s = i % nsets
+        codec.sdpa_int4v(prepared[s], *sets[s][0], *sets[s][1], 1.0, 0, out=out)
+
+    def score_only(i):
+        s = i % nsets
+        codec.score(prepared[s], *sets[s][0])
+
+    ms_step, _, _ = time_launches(torch, step, args.steps, args.warmup)
+    ms_attn, _, _ = time_launches(torch, attn_only, args.steps, args.warmup)
+    ms_score, _, _ = time_launches(torch, score_only, args.steps, args.warmup)
+    score_bytes = Hkv * L * 68 + 2 * Hq * D * 4 + Hq * L * 4
+    gbs = nbytes / (ms_step * 1e-3) / 1e9
+    gbs_attn = nbytes / (ms_attn * 1e-3) / 1e9
+    emit({"metric": "PolarQuant+QJL compressed-key decode attention GB/s at 32k ctx",
+          "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+          "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+          "us_per_layer": round(ms_step * 1e3, 2), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+          "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+          "dtype": "polar7 angles + 128-bit QJL sketch (fp16 norms), int4 V (fp16 scale/bias), "
+                   "f32 q, f32 accumulate",
+          "data": f"synthetic (seeded N(0,1) K/V/q, seeded orthogonal P and N(0,1) S); "
+                  f"{nsets} rotated KV sets",
+          "config": {"workload": f"polar7+QJL decode layer Hq={Hq} Hkv={Hkv} D={D} L={L} "
+                                 "(BASELINE configs[4])", "global_batch": 1, "seq_len": L,
+                     "parallelism": "none (1 GPU)"},
+          "roofline": {"bound": "hbm", "achieved": round(gbs_attn, 1), "peak": PEAK_GBS,
+                       "unit": "GB/s", "frac": round(gbs_attn / PEAK_GBS, 4), "traffic": None,
+                       "kernel": "polar7_sdpa_kernel<2,__half>", "bytes_per_launch": nbytes,
+                       "us_per_launch": round(ms_attn * 1e3, 2)},
+          "score_only": {"us_per_launch": round(ms_score * 1e3, 2), "bytes_per_launch": score_bytes,
+                         "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1)}}, args)
 
 
 def emit(line, args):

@@ -50,6 +50,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 // sqrt(pi/2) / m
 constexpr float kQjlCoef = 0.009791516697777346f;
 constexpr int kP7Words = 12;
+// query heads per workgroup of the polar7 kernels (tables: 20 KB of LDS per head)
+constexpr int kP7MaxG = 2;
 
 // atan2(y, x) in (-pi, pi]: |t| = min/max of |x|, |y|, reduced with
 // atan(t) = pi/4 + atan((t-1)/(t+1)) above tan(pi/8), then the Taylor series
@@ -666,9 +668,14 @@ __global__ __launch_bounds__(128) void rotate128_kernel(const float* x, const fl
 
 // ---- polar7 scores ------------------------------------------------------------
 
+// Per-head query tables written by polar7_prepare_kernel, kP7QTab floats per
+// head: t1 [64][16] (level 1: q'[2j] cos c1_k + q'[2j+1] sin c1_k), tq
+// [16][256] (QJL: sum of (S q')_{8 pos + i} over the set bits i of a byte),
+// then U = sum of S q' (and padding to a 16-byte multiple).
+constexpr int kP7QTab = 1024 + 4096 + 16;
+
 struct P7Keys {
-  const float* qp;        // [Hq][128] rotated query q' = P q
-  const float* qs;        // [Hq][128] S q'
+  const float* qtab;      // [Hq][kP7QTab]
   const float* cs;        // cs1[16][2] then cs2[4][2]
   const uint32_t* angles; // [Hkv][cap][12]
   const uint32_t* norms;  // [Hkv][cap]
@@ -676,148 +683,246 @@ struct P7Keys {
   float* scores;          // [Hq][n] (score only)
 };
 
+// Per-workgroup LDS tables (every entry of t1 / tq / U multiplied by the
+// score scale):
+//   t1[g][j][c] = q'[2j] cos c1_c + q'[2j+1] sin c1_c  (level 1, per head)
+//   tq[g][pos][b] = sum of (S q')_{8 pos + i} over the set bits i of b
+//   t2[kp | k0 << 2 | k1 << 4] = the four grandchild factors of a level pair
+//     with code kp whose child pairs have codes k0, k1:
+//     (cos_p cos_0, cos_p sin_0, sin_p cos_1, sin_p sin_1) -- two levels of
+//     the top-down decode per lookup (levels 7-6, 5-4, 3-2).
 template <int G>
 struct P7Tables {
   float t1[G][64][16];
   float tq[G][16][256];
-  float2 cs2[4];
+  float4 t2[64];
   float U[G];
 };
 
-// Builds the per-head tables of heads h0 .. h0+G-1 (all threads; the caller
-// synchronises).  Every entry is multiplied by sc.
+// Copies the query tables of heads h0 .. h0+G-1 into LDS and builds the
+// combined two-level table t2[kp | k0 << 2 | k1 << 4] = (cos_p cos_0,
+// cos_p sin_0, sin_p cos_1, sin_p sin_1) of the levels 2-7 codebook: the
+// four grandchild factors of a pair with code kp whose child pairs have
+// codes k0, k1 (two levels of the top-down decode per lookup).  All NT
+// threads call it; it ends with a barrier.
 template <int G, int NT>
-__device__ __forceinline__ void build_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0, float sc) {
-  for (int i = threadIdx.x; i < G * 1024; i += NT) {
-    const int g = i >> 10, j = (i >> 4) & 63, c = i & 15;
-    const float* q = k.qp + static_cast<int64_t>(h0 + g) * 128;
-    T.t1[g][j][c] = sc * (q[2 * j] * k.cs[2 * c] + q[2 * j + 1] * k.cs[2 * c + 1]);
+__device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0) {
+  constexpr int kVec = kP7QTab / 4;
+  for (int i = threadIdx.x; i < G * kVec; i += NT) {
+    const int g = i / kVec, r = i - (i / kVec) * kVec;
+    const float4 v = reinterpret_cast<const float4*>(k.qtab + static_cast<int64_t>(h0 + g) * kP7QTab)[r];
+    if (r < 256) reinterpret_cast<float4*>(&T.t1[g][0][0])[r] = v;
+    else if (r < 1280) reinterpret_cast<float4*>(&T.tq[g][0][0])[r - 256] = v;
+    else if (r == 1280) T.U[g] = v.x;
   }
-  for (int i = threadIdx.x; i < G * 4096; i += NT) {
-    const int g = i >> 12, pos = (i >> 8) & 15, bits = i & 255;
-    const float* u = k.qs + static_cast<int64_t>(h0 + g) * 128 + 8 * pos;
-    float s = 0.0f;
+  if (threadIdx.x < 64) {
+    const int kp = threadIdx.x & 3, k0 = (threadIdx.x >> 2) & 3, k1 = threadIdx.x >> 4;
+    const float* c2 = k.cs + 32;
+    const float cp = c2[2 * kp], sp = c2[2 * kp + 1];
+    T.t2[threadIdx.x] = make_float4(cp * c2[2 * k0], cp * c2[2 * k0 + 1], sp * c2[2 * k1],
+                                    sp * c2[2 * k1 + 1]);
+  }
+  __syncthreads();
+}
+
+// q' = P q (or q), u = S q', and the tables of one head per workgroup.
+__global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, const float* P,
+                                                             const float* S, const float* cs,
+                                                             float* qtab, float* q_rot,
+                                                             float* q_sketch) {
+  __shared__ float xs[128], qp[128], u[128], csl[40];
+  const int h = blockIdx.x, t = threadIdx.x;
+  if (t < 128) xs[t] = q[static_cast<int64_t>(h) * 128 + t];
+  if (t < 40) csl[t] = cs[t];
+  __syncthreads();
+  if (t < 128) {
+    float acc = xs[t];
+    if (P) {
+      acc = 0.0f;
+      const float* pr = P + t * 128;
+      for (int d = 0; d < 128; d += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(pr + d);
+        acc = fmaf(xs[d], a.x, acc);
+        acc = fmaf(xs[d + 1], a.y, acc);
+        acc = fmaf(xs[d + 2], a.z, acc);
+        acc = fmaf(xs[d + 3], a.w, acc);
+      }
+    }
+    qp[t] = acc;
+    if (q_rot) q_rot[static_cast<int64_t>(h) * 128 + t] = acc;
+  }
+  __syncthreads();
+  if (t < 128) {
+    const float* sr = S + t * 128;
+    float acc = 0.0f;
+    for (int d = 0; d < 128; d += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(sr + d);
+      acc = fmaf(qp[d], a.x, acc);
+      acc = fmaf(qp[d + 1], a.y, acc);
+      acc = fmaf(qp[d + 2], a.z, acc);
+      acc = fmaf(qp[d + 3], a.w, acc);
+    }
+    u[t] = acc;
+    if (q_sketch) q_sketch[static_cast<int64_t>(h) * 128 + t] = acc;
+  }
+  __syncthreads();
+  float* out = qtab + static_cast<int64_t>(h) * kP7QTab;
+  for (int i = t; i < 1024; i += 256) {
+    const int j = i >> 4, c = i & 15;
+    out[i] = qp[2 * j] * csl[2 * c] + qp[2 * j + 1] * csl[2 * c + 1];
+  }
+  for (int i = t; i < 4096; i += 256) {
+    const int pos = i >> 8, bits = i & 255;
+    float sum = 0.0f;
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-      if ((bits >> b) & 1) s += u[b];
-    T.tq[g][pos][bits] = sc * s;
+    for (int b = 0; b < 8; ++b) sum += ((bits >> b) & 1) ? u[8 * pos + b] : 0.0f;
+    out[1024 + i] = sum;
   }
-  if (threadIdx.x < 4)
-    T.cs2[threadIdx.x] = make_float2(k.cs[32 + 2 * threadIdx.x], k.cs[33 + 2 * threadIdx.x]);
-  if (threadIdx.x >= 64 && threadIdx.x < 64 + G) {
-    const int g = threadIdx.x - 64;
-    const float* u = k.qs + static_cast<int64_t>(h0 + g) * 128;
-    float s = 0.0f;
-    for (int i = 0; i < 128; ++i) s += u[i];
-    T.U[g] = sc * s;
+  if (t < 64) {
+    const float sum = wave_sum_f(u[t] + u[t + 64]);
+    if (t < 16) out[5120 + t] = t == 0 ? sum : 0.0f;
   }
 }
 
-// Score of one key (its 12 angle words, norms word and sketch words) for the
-// G heads of the tables: sum_j r1_j t1[j][n_j] + coef ||r|| (2 sum tq - U).
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+struct P7Quarter {
+  uint32_t l1[2];  // level-1 angle words 2qt, 2qt+1
+  uint32_t l2;     // level-2 word 8 + qt/2
+  uint32_t w10, w11;
+  uint32_t qj;     // QJL word qt
+  uint32_t nrm;
+};
+
+__device__ __forceinline__ void load_p7_quarter(const P7Keys& k, int64_t row, int qt, P7Quarter& Q) {
+  const uint32_t* a = k.angles + row * kP7Words;
+  const u32x2v l1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(a + 2 * qt));
+  Q.l1[0] = l1.x;
+  Q.l1[1] = l1.y;
+  Q.l2 = __builtin_nontemporal_load(a + 8 + (qt >> 1));
+  const u32x2v hi = __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(a + 10));
+  Q.w10 = hi.x;
+  Q.w11 = hi.y;
+  Q.qj = __builtin_nontemporal_load(k.qjl + row * 4 + qt);
+  Q.nrm = __builtin_nontemporal_load(k.norms + row);
+}
+
+__device__ __forceinline__ float pick4(const float4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Quarter qt's part of the score of one key for the G heads of the tables;
+// the four quarters (lanes 4m .. 4m+3) sum to
+// sc * (sum_j r1_j t1[j][n_j] + coef ||r|| (2 sum tq - U)).
 template <int G>
-__device__ __forceinline__ void p7_score(const P7Tables<G>& T, const uint32_t w[12], uint32_t nrm,
-                                         const uint32_t qj[4], float out[G]) {
-  const float R = h2f_lo(nrm), rn = h2f_hi(nrm);
-  float r6[2], r5[4], r4[8], r3[16];
-  {
-    const float2 c = T.cs2[(w[11] >> 28) & 3];
-    r6[0] = R * c.x;
-    r6[1] = R * c.y;
+__device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Quarter& Q, int qt,
+                                                 float sc, float out[G]) {
+  const uint32_t w11 = Q.w11, w10 = Q.w10;
+  const float4 ta = T.t2[((w11 >> 28) & 3u) | ((w11 >> 22) & 0x3Cu)];
+  const float4 tb = T.t2[((w11 >> (16 + 2 * qt)) & 3u) | (((w11 >> (4 * qt)) & 15u) << 2)];
+  float4 tc[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+    tc[ii] = T.t2[((w10 >> (8 * qt + 2 * ii)) & 3u) | (((Q.l2 >> (16 * (qt & 1) + 4 * ii)) & 15u) << 2)];
+  float qa[G], acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    qa[g] = 0.0f;
+    acc[g] = 0.0f;
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const float2 c = T.cs2[(w[11] >> (24 + 2 * j)) & 3];
-    r5[2 * j] = r6[j] * c.x;
-    r5[2 * j + 1] = r6[j] * c.y;
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (Q.qj >> (8 * b)) & 255u;
+#pragma unroll
+    for (int g = 0; g < G; ++g) qa[g] += T.tq[g][4 * qt + b][byte];
   }
+  const float R = h2f_lo(Q.nrm), rn = h2f_hi(Q.nrm);
+  const float r5 = R * pick4(ta, qt);
+  const float r3[4] = {r5 * tb.x, r5 * tb.y, r5 * tb.z, r5 * tb.w};
+  const float* t1 = &T.t1[0][16 * qt][0];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float2 c = T.cs2[(w[11] >> (16 + 2 * j)) & 3];
-    r4[2 * j] = r5[j] * c.x;
-    r4[2 * j + 1] = r5[j] * c.y;
-  }
+  for (int ii = 0; ii < 4; ++ii) {
+    const float r1[4] = {r3[ii] * tc[ii].x, r3[ii] * tc[ii].y, r3[ii] * tc[ii].z, r3[ii] * tc[ii].w};
+    const uint32_t word = Q.l1[ii >> 1];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float2 c = T.cs2[(w[11] >> (2 * j)) & 3];
-    r3[2 * j] = r4[j] * c.x;
-    r3[2 * j + 1] = r4[j] * c.y;
-  }
-  float acc[G];
+    for (int e = 0; e < 4; ++e) {
+      const int jj = 4 * ii + e;  // level-1 pair 16 qt + jj
+      const uint32_t nib = (word >> (4 * (jj % 8))) & 15u;
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g] = 0.0f;
-#pragma unroll
-  for (int j3 = 0; j3 < 16; ++j3) {
-    const float2 c3 = T.cs2[(w[10] >> (2 * j3)) & 3];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int j2 = 2 * j3 + e;
-      const float r2 = e ? r3[j3] * c3.y : r3[j3] * c3.x;
-      const float2 c2 = T.cs2[(w[8 + j2 / 16] >> (2 * (j2 % 16))) & 3];
-      const float r1a = r2 * c2.x, r1b = r2 * c2.y;
-      const int ja = 2 * j2, jb = 2 * j2 + 1;
-      const uint32_t na = (w[ja / 8] >> (4 * (ja % 8))) & 15;
-      const uint32_t nb = (w[jb / 8] >> (4 * (jb % 8))) & 15;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        acc[g] = fmaf(r1a, T.t1[g][ja][na], acc[g]);
-        acc[g] = fmaf(r1b, T.t1[g][jb][nb], acc[g]);
-      }
+      for (int g = 0; g < G; ++g) acc[g] = fmaf(r1[e], t1[g * 1024 + jj * 16 + nib], acc[g]);
     }
-  }
-  float qa[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) qa[g] = 0.0f;
-#pragma unroll
-  for (int pos = 0; pos < 16; ++pos) {
-    const uint32_t byte = (qj[pos / 4] >> (8 * (pos % 4))) & 255;
-#pragma unroll
-    for (int g = 0; g < G; ++g) qa[g] += T.tq[g][pos][byte];
   }
   const float cr = kQjlCoef * rn;
 #pragma unroll
-  for (int g = 0; g < G; ++g) out[g] = fmaf(cr, 2.0f * qa[g] - T.U[g], acc[g]);
+  for (int g = 0; g < G; ++g) out[g] = sc * fmaf(cr, 2.0f * qa[g] - (qt == 0 ? T.U[g] : 0.0f), acc[g]);
 }
 
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void load_p7_key(const P7Keys& k, int64_t row, uint32_t w[12],
-                                            uint32_t& nrm, uint32_t qj[4]) {
-  const u32x4v* a = reinterpret_cast<const u32x4v*>(k.angles + row * kP7Words);
+// Full scores in all four lanes of each key.
+template <int G>
+__device__ __forceinline__ void quarter_sum(float s[G]) {
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const u32x4v u = __builtin_nontemporal_load(a + i);
-    w[4 * i] = u.x; w[4 * i + 1] = u.y; w[4 * i + 2] = u.z; w[4 * i + 3] = u.w;
+  for (int g = 0; g < G; ++g) {
+    s[g] += shfl_xor_f(s[g], 1);
+    s[g] += shfl_xor_f(s[g], 2);
   }
-  nrm = __builtin_nontemporal_load(k.norms + row);
-  const u32x4v u = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(k.qjl + row * 4));
-  qj[0] = u.x; qj[1] = u.y; qj[2] = u.z; qj[3] = u.w;
 }
 
-// Scores only (the compressed_score of configs[4]): one key per thread, 1024
-// keys per workgroup; grid (key blocks, kv heads * head subgroups).
+// Scores only (the compressed_score of configs[4]): four lanes per key, 64
+// keys per pass of a 256-thread workgroup, 1024 keys per workgroup; the next
+// pass's words are loaded while the current pass is scored.  Grid (key
+// blocks, kv heads * head subgroups).
 template <int G>
 __global__ __launch_bounds__(256) void polar7_score_kernel(P7Keys k, int n, int cap, int gqa,
                                                            int n_sub, float scale) {
   __shared__ P7Tables<G> T;
   const int hy = blockIdx.y, kvh = hy / n_sub, sub = hy - (hy / n_sub) * n_sub;
   const int h0 = kvh * gqa + sub * G;
-  build_p7_tables<G, 256>(T, k, h0, scale);
-  __syncthreads();
-  for (int t = blockIdx.x * 1024 + threadIdx.x; t < min(n, (blockIdx.x + 1) * 1024); t += 256) {
-    uint32_t w[12], nrm, qj[4];
-    load_p7_key(k, static_cast<int64_t>(kvh) * cap + t, w, nrm, qj);
+  const int qt = threadIdx.x & 3, key = threadIdx.x >> 2;  // key 0..63 of a pass
+  const int t0 = blockIdx.x * 1024 + key;
+  const int last = n - 1;
+  const int64_t rowbase = static_cast<int64_t>(kvh) * cap;
+  const int npass = min(16, (n - blockIdx.x * 1024 + 63) / 64);
+  P7Quarter A, B;
+  load_p7_quarter(k, rowbase + min(t0, last), qt, A);
+  load_p7_tables<G, 256>(T, k, h0);
+  auto pass = [&](const P7Quarter& Q, int r) {
     float s[G];
-    p7_score<G>(T, w, nrm, qj, s);
+    p7_quarter_score<G>(T, Q, qt, scale, s);
+    quarter_sum<G>(s);
+    const int t = t0 + 64 * r;
+    if (qt < G && t < n) {
+      float v = s[0];
 #pragma unroll
-    for (int g = 0; g < G; ++g) k.scores[static_cast<int64_t>(h0 + g) * n + t] = s[g];
+      for (int g = 1; g < G; ++g) v = qt == g ? s[g] : v;
+      k.scores[static_cast<int64_t>(h0 + qt) * n + t] = v;
+    }
+  };
+  for (int r = 0; r < npass; r += 2) {
+    load_p7_quarter(k, rowbase + min(t0 + 64 * (r + 1), last), qt, B);
+    pass(A, r);
+    load_p7_quarter(k, rowbase + min(t0 + 64 * (r + 2), last), qt, A);
+    if (r + 1 < npass) pass(B, r + 1);
   }
 }
 
+template <typename SB>
+__device__ __forceinline__ float2 sb_pair(const uint32_t* w);
+template <>
+__device__ __forceinline__ float2 sb_pair<__half>(const uint32_t* w) {
+  return make_float2(h2f_lo(w[0]), h2f_hi(w[0]));
+}
+template <>
+__device__ __forceinline__ float2 sb_pair<float>(const uint32_t* w) {
+  return make_float2(__uint_as_float(w[0]), __uint_as_float(w[1]));
+}
+
 // configs[4] attention: polar7 + QJL scores, softmax, int4 V (group 64,
-// scale/bias SB), split-K.  Per 64-key tile of a wave: one key per lane for
-// the scores; then 16 steps of 4 keys x 16 words for V (lane: key 4*step +
-// lane/16, dims 8*(lane%16) .. +7), weights read back from LDS.
+// scale/bias SB), split-K.  Per 64-key tile of a wave: four lanes per key
+// for the scores (4 sub-tiles of 16 keys); the weights and the V scale/bias
+// of key `lane` go through LDS; then
+// 16 steps of 4 keys x 16 words for V (lane: key 4*step + lane/16, dims
+// 8*(lane%16) .. +7).  Key words are loaded one tile ahead; the V words of a
+// tile are issued before its scores are computed.
 template <int G, typename SB>
 __global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
   constexpr int NW = 4, D = 128;
@@ -825,18 +930,31 @@ __global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k
   using Fin = Finalize<G, D, NW>;
   __shared__ float arena[Fin::kArena];
   __shared__ float p_lds[NW][G][64];
+  __shared__ float2 sb_lds[NW][64][2];  // [wave][key][group] = (scale, bias)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hy = blockIdx.y, split = blockIdx.x;
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
   const int h0 = kvh * p.gqa + sub * G;
   const SplitRange rg = split_range(p, 0, split);
   if (split >= rg.S) return;
-  build_p7_tables<G, NW * 64>(T, k, h0, p.scale_log2);
-  __syncthreads();
-
-  const SB* vs = static_cast<const SB*>(p.vs);
-  const SB* vb = static_cast<const SB*>(p.vb);
   const int wd = lane & 15, kg = lane >> 4, gq = wd >> 3;
+  const int64_t rowbase = static_cast<int64_t>(kvh) * p.cap;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int base0 = rg.t_begin + wv * 64;
+  const int last = rg.t_end - 1;
+  const int ntile = base0 < rg.t_end ? (rg.t_end - base0 + NW * 64 - 1) / (NW * 64) : 0;
+  constexpr int SBW = sizeof(SB) / 2;  // words of one row's two scales (or biases)
+  // scoring layout: four lanes per key (quarter qt = lane & 3), the 64 keys
+  // of a tile as 4 sub-tiles u of 16 keys: key 16u + (lane >> 2)
+  const int qt = lane & 3, kq = lane >> 2;
+  P7Quarter keyA[4], keyB[4];
+  auto load_keys = [&](P7Quarter* Q, int tb) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_p7_quarter(k, rowbase + min(tb + 16 * u + kq, last), qt, Q[u]);
+  };
+  if (ntile > 0) load_keys(keyA, base0);
+  load_p7_tables<G, NW * 64>(T, k, h0);
+
   float m_run[G], l_run[G], acc[G][8], accb[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -846,19 +964,33 @@ __global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
   }
-  const int64_t rowbase = static_cast<int64_t>(kvh) * p.cap;
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  for (int tb = rg.t_begin + wv * 64; tb < rg.t_end; tb += NW * 64) {
-    const bool valid = tb + lane < rg.t_end;
-    const int t = min(tb + lane, rg.t_end - 1);
-    uint32_t w[12], nrm, qj[4];
-    load_p7_key(k, rowbase + t, w, nrm, qj);
-    float s[G];
-    p7_score<G>(T, w, nrm, qj, s);
+
+  auto process = [&](const P7Quarter* K, int tb) {
+    // V words of the tile (consumed after the scores, which hide their latency)
+    const int64_t row = rowbase + min(tb + lane, last);
+    uint32_t vsw[SBW], vbw[SBW], vw[16];
+#pragma unroll
+    for (int i = 0; i < SBW; ++i) {
+      vsw[i] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p.vs) + row * SBW + i);
+      vbw[i] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p.vb) + row * SBW + i);
+    }
+#pragma unroll
+    for (int st = 0; st < 16; ++st)
+      vw[st] = __builtin_nontemporal_load(p.vq + (rowbase + min(tb + 4 * st + kg, last)) * 16 + wd);
+    float s[4][G];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      p7_quarter_score<G>(T, K[u], qt, p.scale_log2, s[u]);
+      quarter_sum<G>(s[u]);
+      const bool valid = tb + 16 * u + kq < rg.t_end;
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[u][g] = valid ? s[u][g] : -INFINITY;
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float sv = valid ? s[g] : -INFINITY;
-      const float m_new = fmaxf(m_run[g], wave_max_f(sv));
+      const float mt = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
+      const float m_new = fmaxf(m_run[g], wave_max_f(mt));
       if (m_new > m_run[g]) {  // wave-uniform
         const float f = merge_factor(m_run[g], m_new);
         l_run[g] *= f;
@@ -867,18 +999,24 @@ __global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k
         for (int j = 0; j < 8; ++j) acc[g][j] *= f;
         m_run[g] = m_new;
       }
-      const float pw = valid ? fast_exp2(sv - m_run[g]) : 0.0f;
-      l_run[g] += pw;
-      p_lds[wave][g][lane] = pw;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float pw = s[u][g] == -INFINITY ? 0.0f : fast_exp2(s[u][g] - m_run[g]);
+        if (qt == 0) {
+          l_run[g] += pw;
+          p_lds[wave][g][16 * u + kq] = pw;
+        }
+      }
     }
+    const float2 sc2 = sb_pair<SB>(vsw), bi2 = sb_pair<SB>(vbw);
+    sb_lds[wave][lane][0] = make_float2(sc2.x, bi2.x);
+    sb_lds[wave][lane][1] = make_float2(sc2.y, bi2.y);
     wave_lds_sync();
-#pragma unroll 4
+#pragma unroll
     for (int st = 0; st < 16; ++st) {
       const int kk = 4 * st + kg;
-      const int64_t vrow = rowbase + min(tb + kk, rg.t_end - 1);
-      const uint32_t wv4 = __builtin_nontemporal_load(p.vq + vrow * 16 + wd);
-      const float sc = sb_to_f32(vs[vrow * 2 + gq]);
-      const float bi = sb_to_f32(vb[vrow * 2 + gq]);
+      const float2 sbv = sb_lds[wave][kk][gq];
+      const uint32_t wv4 = vw[st];
       const uint32_t lo = wv4 & 0x0F0F0F0Fu, hi = (wv4 >> 4) & 0x0F0F0F0Fu;
       float nv[8];
 #pragma unroll
@@ -889,14 +1027,22 @@ __global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float pg = p_lds[wave][g][kk];
-        const float ps = pg * sc;
+        const float ps = pg * sbv.x;
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(ps, nv[j], acc[g][j]);
-        accb[g] = fmaf(pg, bi, accb[g]);
+        accb[g] = fmaf(pg, sbv.y, accb[g]);
       }
     }
     wave_lds_sync();
+  };
+
+  for (int it = 0; it < ntile; it += 2) {
+    load_keys(keyB, min(base0 + (it + 1) * NW * 64, last));
+    process(keyA, base0 + it * NW * 64);
+    load_keys(keyA, min(base0 + (it + 2) * NW * 64, last));
+    if (it + 1 < ntile) process(keyB, base0 + (it + 1) * NW * 64);
   }
+
   // sum the four key groups of each dimension slice, then one lane per slice
   // writes its 8 dims (the bias term belongs to the slice's quant group)
 #pragma unroll
@@ -1158,15 +1304,15 @@ int polar_sdpa_params(SdpaParams& p, int Hq, int Hkv, int D, int n, int cap, flo
   return TQ_OK;
 }
 
-int p7_keys_setup(P7Keys& k, const float* qp, const float* qs, const uint32_t* angles,
-                  const uint32_t* norms, const uint32_t* qjl, const float* cs_tables, int Hq,
-                  int Hkv, const char* fn) {
-  TQ_CHECK_ARG(qp && qs && angles && norms && qjl && cs_tables, "%s: null pointer", fn);
+int p7_keys_setup(P7Keys& k, const float* q_tables, const uint32_t* angles, const uint32_t* norms,
+                  const uint32_t* qjl, const float* cs_tables, int Hq, int Hkv, const char* fn) {
+  TQ_CHECK_ARG(q_tables && angles && norms && qjl && cs_tables, "%s: null pointer", fn);
   TQ_CHECK_ARG(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "%s: num_heads must be a multiple of num_kv_heads", fn);
-  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(angles) % 16 == 0 && reinterpret_cast<uintptr_t>(qjl) % 16 == 0,
-               "%s: angles / qjl must be 16-byte aligned", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(angles) % 16 == 0 && reinterpret_cast<uintptr_t>(qjl) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(q_tables) % 16 == 0,
+               "%s: angles / qjl / q_tables must be 16-byte aligned", fn);
   k = P7Keys{};
-  k.qp = qp; k.qs = qs; k.cs = cs_tables;
+  k.qtab = q_tables; k.cs = cs_tables;
   k.angles = angles; k.norms = norms; k.qjl = qjl;
   return TQ_OK;
 }
@@ -1343,38 +1489,48 @@ int tq_polar7_kv_append(const float* k_new, const float* precondition, const flo
   return TQ_OK;
 }
 
-int tq_polar7_score(const float* q_rot, const float* q_sketch, const uint32_t* angles,
-                    const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
-                    int num_heads, int num_kv_heads, int kv_len, int kv_capacity, float scale,
-                    float* scores, void* stream) {
+int tq_polar7_prepare_query(const float* q, const float* precondition, const float* sketch,
+                            const float* cs_tables, int num_heads, float* q_tables, float* q_rot,
+                            float* q_sketch, void* stream) {
+  const char* fn = "tq_polar7_prepare_query";
+  TQ_CHECK_ARG(q && sketch && cs_tables && q_tables, "%s: null pointer", fn);
+  TQ_CHECK_ARG(num_heads >= 0 && num_heads <= 65535, "%s: bad num_heads", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(q_tables) % 16 == 0, "%s: q_tables must be 16-byte aligned", fn);
+  if (num_heads == 0) return TQ_OK;
+  polar7_prepare_kernel<<<num_heads, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      q, precondition, sketch, cs_tables, q_tables, q_rot, q_sketch);
+  TQ_CHECK_LAUNCH("polar7_prepare_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_t* norms,
+                    const uint32_t* qjl, const float* cs_tables, int num_heads, int num_kv_heads,
+                    int kv_len, int kv_capacity, float scale, float* scores, void* stream) {
   const char* fn = "tq_polar7_score";
   P7Keys k;
-  int st = p7_keys_setup(k, q_rot, q_sketch, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
+  int st = p7_keys_setup(k, q_tables, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
   if (st != TQ_OK) return st;
   TQ_CHECK_ARG(scores != nullptr, "%s: scores is NULL", fn);
   TQ_CHECK_ARG(kv_len >= 0 && kv_capacity >= 1 && kv_len <= kv_capacity, "%s: bad kv_len", fn);
   TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
   if (kv_len == 0) return TQ_OK;
   k.scores = scores;
-  const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, 4), n_sub = gqa / G;
+  const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, kP7MaxG), n_sub = gqa / G;
   TQ_CHECK_ARG(num_kv_heads * n_sub <= 65535, "%s: too many heads", fn);
   dim3 grid((kv_len + 1023) / 1024, num_kv_heads * n_sub);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (G) {
-    case 1: polar7_score_kernel<1><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale); break;
-    case 2: polar7_score_kernel<2><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale); break;
-    default: polar7_score_kernel<4><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale); break;
-  }
+  if (G == 1) polar7_score_kernel<1><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  else polar7_score_kernel<2><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
   TQ_CHECK_LAUNCH("polar7_score_kernel");
   return TQ_OK;
 }
 
 size_t tq_polar7_sdpa_workspace_size(int num_heads, int num_kv_heads, int max_kv_len) {
   if (num_kv_heads < 1 || num_heads < num_kv_heads || max_kv_len < 0) return 0;
-  return polar_ws_size(num_heads, num_kv_heads, 128, max_kv_len, 4);
+  return polar_ws_size(num_heads, num_kv_heads, 128, max_kv_len, kP7MaxG);
 }
 
-int tq_polar7_sdpa_int4v(const float* q_rot, const float* q_sketch, const uint32_t* angles,
+int tq_polar7_sdpa_int4v(const float* q_tables, const uint32_t* angles,
                          const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
                          const uint32_t* v_quant, const void* v_scales, const void* v_biases,
                          tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
@@ -1382,7 +1538,7 @@ int tq_polar7_sdpa_int4v(const float* q_rot, const float* q_sketch, const uint32
                          void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "tq_polar7_sdpa_int4v";
   P7Keys k;
-  int st = p7_keys_setup(k, q_rot, q_sketch, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
+  int st = p7_keys_setup(k, q_tables, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
   if (st != TQ_OK) return st;
   TQ_CHECK_ARG(v_quant && v_scales && v_biases, "%s: null V pointer", fn);
   TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32, "%s: sb_dtype must be f16 or f32", fn);
@@ -1390,19 +1546,17 @@ int tq_polar7_sdpa_int4v(const float* q_rot, const float* q_sketch, const uint32
   dim3 grid;
   int G = 1;
   st = polar_sdpa_params(p, num_heads, num_kv_heads, 128, kv_len, kv_capacity, scale, sliding_window,
-                         0.0f, 4, out, workspace, workspace_bytes, grid, G, fn);
+                         0.0f, kP7MaxG, out, workspace, workspace_bytes, grid, G, fn);
   if (st != TQ_OK) return st;
   p.vq = v_quant; p.vs = v_scales; p.vb = v_biases;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = sb_dtype == TQ_F16;
   if (f16) {
     if (G == 1) polar7_sdpa_kernel<1, __half><<<grid, 256, 0, s>>>(p, k);
-    else if (G == 2) polar7_sdpa_kernel<2, __half><<<grid, 256, 0, s>>>(p, k);
-    else polar7_sdpa_kernel<4, __half><<<grid, 256, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<2, __half><<<grid, 256, 0, s>>>(p, k);
   } else {
     if (G == 1) polar7_sdpa_kernel<1, float><<<grid, 256, 0, s>>>(p, k);
-    else if (G == 2) polar7_sdpa_kernel<2, float><<<grid, 256, 0, s>>>(p, k);
-    else polar7_sdpa_kernel<4, float><<<grid, 256, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<2, float><<<grid, 256, 0, s>>>(p, k);
   }
   TQ_CHECK_LAUNCH("polar7_sdpa_kernel");
   return TQ_OK;

@@ -23,6 +23,7 @@ from .turboquant import _check_cuda, _need, _ptr, _stream, workspace
 P7_D = 128
 P7_WORDS = 12
 QJL_M = 128
+P7_QTAB = 5136  # floats of per-head query tables (TQ_POLAR7_QTAB)
 
 
 def _codebooks(cbs: Sequence[torch.Tensor]):
@@ -298,33 +299,37 @@ class Polar7Codec:
              _ptr(self.cs), _ptr(angles), _ptr(norms), _ptr(qjl), B, Hkv, cap, _ptr(positions), T,
              _stream(stream))
 
-    def prepare_query(self, q: torch.Tensor, stream=None):
-        """(q' = P q, S q') for q (Hq, 128) f32."""
+    def prepare_query(self, q: torch.Tensor, *, with_vectors: bool = False, stream=None):
+        """Query side of a decode step for q (Hq, 128) f32: the per-head
+        tables the score kernels read ((Hq, TQ_POLAR7_QTAB) f32).  With
+        ``with_vectors`` also returns q' = P q and S q' ((Hq, 128) each)."""
         _check_cuda("q", q)
+        _need(q.dim() == 2 and q.shape[1] == P7_D and q.dtype == torch.float32, "q must be (Hq, 128) f32")
         Hq = q.shape[0]
-        if self.P is not None:
-            qp = torch.empty_like(q)
-            call("tq_polar_rotate", _ptr(q), _ptr(self.P), Hq, P7_D, _ptr(qp), _stream(stream))
-        else:
-            qp = q
-        qs = torch.empty_like(q)
-        call("tq_qjl_query", _ptr(qp), _ptr(self.S), Hq, _ptr(qs), _stream(stream))
-        return qp, qs
+        tab = torch.empty((Hq, P7_QTAB), dtype=torch.float32, device=q.device)
+        qp = torch.empty_like(q) if with_vectors else None
+        qs = torch.empty_like(q) if with_vectors else None
+        call("tq_polar7_prepare_query", _ptr(q), _ptr(self.P), _ptr(self.S), _ptr(self.cs), Hq,
+             _ptr(tab), _ptr(qp), _ptr(qs), _stream(stream))
+        return (tab, qp, qs) if with_vectors else tab
 
-    def score(self, q_rot, q_sketch, angles, norms, qjl, scale: float = 1.0, *,
+    def score(self, q_tables, angles, norms, qjl, scale: float = 1.0, *,
               kv_len: Optional[int] = None, stream=None) -> torch.Tensor:
-        Hq = q_rot.shape[0]
+        """(Hq, kv_len) scores of the keys in the caches (Hkv, cap, .)."""
+        Hq = q_tables.shape[0]
         Hkv, cap = angles.shape[0], angles.shape[1]
         n = cap if kv_len is None else int(kv_len)
-        out = torch.empty((Hq, n), dtype=torch.float32, device=q_rot.device)
-        call("tq_polar7_score", _ptr(q_rot), _ptr(q_sketch), _ptr(angles), _ptr(norms), _ptr(qjl),
+        out = torch.empty((Hq, n), dtype=torch.float32, device=q_tables.device)
+        call("tq_polar7_score", _ptr(q_tables), _ptr(angles), _ptr(norms), _ptr(qjl),
              _ptr(self.cs), Hq, Hkv, n, cap, float(scale), _ptr(out), _stream(stream))
         return out
 
-    def sdpa_int4v(self, q_rot, q_sketch, angles, norms, qjl, v_quant, v_scales, v_biases,
+    def sdpa_int4v(self, q_tables, angles, norms, qjl, v_quant, v_scales, v_biases,
                    scale: float = 1.0, sliding_window: int = 0, *, kv_len: Optional[int] = None,
                    out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-        Hq = q_rot.shape[0]
+        """Decode attention over the compressed keys with int4 V
+        (Hkv, cap, 16) and scale/bias (Hkv, cap, 2); returns (Hq, 128) f32."""
+        Hq = q_tables.shape[0]
         Hkv, cap = angles.shape[0], angles.shape[1]
         _check_cuda("v_quant", v_quant)
         _need(v_quant.shape == (Hkv, cap, P7_D // 8), "v_quant must be (Hkv, cap, 16)")
@@ -332,11 +337,10 @@ class Polar7Codec:
         sbt = TQ_F16 if v_scales.dtype == torch.float16 else TQ_F32
         n = cap if kv_len is None else int(kv_len)
         if out is None:
-            out = torch.empty((Hq, P7_D), dtype=torch.float32, device=q_rot.device)
+            out = torch.empty((Hq, P7_D), dtype=torch.float32, device=q_tables.device)
         nbytes = _lib.load().tq_polar7_sdpa_workspace_size(Hq, Hkv, n)
-        ws = workspace(nbytes, q_rot.device)
-        call("tq_polar7_sdpa_int4v", _ptr(q_rot), _ptr(q_sketch), _ptr(angles), _ptr(norms),
-             _ptr(qjl), _ptr(self.cs), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt,
-             _ptr(out), Hq, Hkv, n, cap, float(scale), int(sliding_window), _ptr(ws), ws.numel(),
-             _stream(stream))
+        ws = workspace(nbytes, q_tables.device)
+        call("tq_polar7_sdpa_int4v", _ptr(q_tables), _ptr(angles), _ptr(norms), _ptr(qjl),
+             _ptr(self.cs), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out), Hq, Hkv,
+             n, cap, float(scale), int(sliding_window), _ptr(ws), ws.numel(), _stream(stream))
         return out

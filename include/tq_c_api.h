@@ -241,23 +241,34 @@ int tq_polar7_kv_append(const float* k_new, const float* precondition, const flo
                         uint32_t* norms, uint32_t* qjl, int batch, int num_kv_heads,
                         int kv_capacity, const int32_t* positions, int n_new, void* stream);
 /* y = x P^T for rows of 128 (the query rotation q' = P q), and the query
- * sketch S q'. */
+ * sketch S q' (utilities; tq_polar7_prepare_query does both). */
 int tq_polar_rotate(const float* x, const float* precondition, int64_t rows, int dim, float* y,
                     void* stream);
 int tq_qjl_query(const float* q_rot, const float* sketch, int num_heads, float* q_sketch,
                  void* stream);
+
+/* Query side of a decode step: q [num_heads, 128] f32 -> q' = P q
+ * (precondition NULL: q' = q), S q', and the per-head tables the score
+ * kernels read, TQ_POLAR7_QTAB floats per head in q_tables (16-byte
+ * aligned): [64][16] level-1 table q'[2j] cos c_k + q'[2j+1] sin c_k,
+ * [16][256] QJL byte table (sum of (S q')_{8 pos + i} over the set bits i),
+ * then sum(S q') and padding.  q_rot / q_sketch ([num_heads, 128]) are
+ * optional copies of q' and S q' (NULL: not written). */
+#define TQ_POLAR7_QTAB 5136
+int tq_polar7_prepare_query(const float* q, const float* precondition, const float* sketch,
+                            const float* cs_tables, int num_heads, float* q_tables, float* q_rot,
+                            float* q_sketch, void* stream);
 /* scores[h, n] = scale * (<q'_h, yhat_n> + sqrt(pi/2)/128 * ||r_n|| *
  * <S q'_h, sign(S r_n)>) over rows [0, kv_len) of kv head h / gqa. */
-int tq_polar7_score(const float* q_rot, const float* q_sketch, const uint32_t* angles,
-                    const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
-                    int num_heads, int num_kv_heads, int kv_len, int kv_capacity, float scale,
-                    float* scores, void* stream);
+int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_t* norms,
+                    const uint32_t* qjl, const float* cs_tables, int num_heads, int num_kv_heads,
+                    int kv_len, int kv_capacity, float scale, float* scores, void* stream);
 /* Decode attention over those scores (window rule and empty-set rule of
  * tq_sdpa_int4) with int4 V [num_kv_heads, kv_capacity, 16] + scale/bias
  * [.., 2] in sb_dtype; out [num_heads, 128] f32.  Workspace as
  * tq_sdpa_int4. */
 size_t tq_polar7_sdpa_workspace_size(int num_heads, int num_kv_heads, int max_kv_len);
-int tq_polar7_sdpa_int4v(const float* q_rot, const float* q_sketch, const uint32_t* angles,
+int tq_polar7_sdpa_int4v(const float* q_tables, const uint32_t* angles,
                          const uint32_t* norms, const uint32_t* qjl, const float* cs_tables,
                          const uint32_t* v_quant, const void* v_scales, const void* v_biases,
                          tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,

@@ -194,10 +194,20 @@ def test_prepare_query(pq):
     rng, _, P, S = p7_inputs(6, 0)
     q = rng.standard_normal((32, 128)).astype(f32)
     codec = pq.Polar7Codec(dev(P), dev(S))
-    qp, qs = (host(t) for t in codec.prepare_query(dev(q)))
+    tab, qp, qs = (host(t) for t in codec.prepare_query(dev(q), with_vectors=True))
     qp_ref = q.astype(np.float64) @ P.astype(np.float64).T
+    qs_ref = qp_ref @ S.astype(np.float64).T
     assert np.max(np.abs(qp - qp_ref)) < 1e-4
-    assert np.max(np.abs(qs - qp_ref @ S.astype(np.float64).T)) < 1e-3
+    assert np.max(np.abs(qs - qs_ref)) < 1e-3
+    # tables: level-1 dot products, QJL byte subset sums, sum of S q'
+    cb1, _ = PQ.polar7_codebooks()
+    cs1 = PQ.cs_table(cb1).astype(np.float64)
+    t1 = qp_ref[:, 0::2, None] * cs1[:, 0] + qp_ref[:, 1::2, None] * cs1[:, 1]
+    assert np.max(np.abs(tab[:, :1024].reshape(32, 64, 16) - t1)) < 1e-4
+    bits = (np.arange(256)[:, None] >> np.arange(8)) & 1
+    tq = np.einsum("hpi,bi->hpb", qs_ref.reshape(32, 16, 8), bits)
+    assert np.max(np.abs(tab[:, 1024:5120].reshape(32, 16, 256) - tq)) < 1e-3
+    assert np.max(np.abs(tab[:, 5120] - qs_ref.sum(1))) < 1e-2
 
 
 def p7_cache_on_gpu(pq, seed, Hkv, L, rot=True):
@@ -218,13 +228,14 @@ def host_norms(n):
     return n.view(np.uint16).reshape(n.shape + (2,)).view(np.float16)
 
 
-@pytest.mark.parametrize("Hq,Hkv,L", [(32, 16, 2000), (4, 4, 333), (16, 2, 1200)])
-def test_polar7_score(pq, Hq, Hkv, L):
+@pytest.mark.parametrize("Hq,Hkv,L,scale", [(32, 16, 2000, 1.0), (4, 4, 333, 0.3), (16, 2, 1200, 1.0),
+                                            (8, 8, 70, 1.0)])
+def test_polar7_score(pq, Hq, Hkv, L, scale):
     rng, codec, P, S, dk, hk, _ = p7_cache_on_gpu(pq, Hq + L, Hkv, L)
     q = rng.standard_normal((Hq, 128)).astype(f32)
-    qp, qs = codec.prepare_query(dev(q))
-    got = host(codec.score(qp, qs, *dk))
-    ref = PQ.polar7_scores(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], Hq // Hkv)
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    got = host(codec.score(tab, *dk, scale))
+    ref = PQ.polar7_scores(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], Hq // Hkv, scale)
     err = np.abs(got - ref)
     assert err.max() < SCORE_ATOL, f"max score err {err.max():.3e}"
 
@@ -236,8 +247,8 @@ def test_polar7_sdpa_int4v(pq, Hq, Hkv, L, W, sb):
     rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 3 * Hq + L + W, Hkv, L)
     vq, vs, vb = O.quantize_int4(v, sb)
     q = rng.standard_normal((Hq, 128)).astype(f32)
-    qp, qs = codec.prepare_query(dev(q))
-    got = host(codec.sdpa_int4v(qp, qs, *dk, dev(vq), dev(vs), dev(vb), 1.0, W))
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    got = host(codec.sdpa_int4v(tab, *dk, dev(vq), dev(vs), dev(vb), 1.0, W))
     ref = PQ.polar7_sdpa_int4v(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], vq, vs, vb,
                                Hq // Hkv, 1.0, W)
     assert_close(got, ref, f"polar7 sdpa Hq{Hq} Hkv{Hkv} L{L} W{W} {sb}")
@@ -247,11 +258,11 @@ def test_polar7_sdpa_empty_and_prefix(pq):
     rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 77, 2, 300)
     vq, vs, vb = O.quantize_int4(v)
     q = rng.standard_normal((4, 128)).astype(f32)
-    qp, qs = codec.prepare_query(dev(q))
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
     d = [dev(vq), dev(vs), dev(vb)]
-    z = host(codec.sdpa_int4v(qp, qs, *dk, *d, kv_len=0))
+    z = host(codec.sdpa_int4v(tab, *dk, *d, kv_len=0))
     assert not z.any()
-    got = host(codec.sdpa_int4v(qp, qs, *dk, *d, kv_len=123))
+    got = host(codec.sdpa_int4v(tab, *dk, *d, kv_len=123))
     ref = PQ.polar7_sdpa_int4v(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], vq, vs, vb, 2,
                                kv_len=123)
     assert_close(got, ref, "prefix 123")
@@ -264,8 +275,8 @@ def test_polar7_full_size_two_heads(pq):
     rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 2026, Hkv, L)
     vq, vs, vb = O.quantize_int4(v)
     q = rng.standard_normal((Hq, 128)).astype(f32)
-    qp, qs = codec.prepare_query(dev(q))
-    got = host(codec.sdpa_int4v(qp, qs, *dk, dev(vq), dev(vs), dev(vb)))
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    got = host(codec.sdpa_int4v(tab, *dk, dev(vq), dev(vs), dev(vb)))
     hqp, hqs = host(qp), host(qs)
     for kvh in (0, 11):
         sl = slice(kvh, kvh + 1)
