@@ -41,7 +41,9 @@ def _compile(src: str) -> str:
     if src.endswith(".hip"):
         cmd = [_hipcc(), *COMMON, *HIP_FLAGS, "-c", path, "-o", obj]
     else:
-        cmd = [_hipcc(), *COMMON, "-x", "c++", "-c", path, "-o", obj]
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        cmd = [_hipcc(), *COMMON, "-x", "c++", "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include",
+               "-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in r.stderr.splitlines()
                      if "packed-fp32-ops" not in l)
@@ -50,6 +52,26 @@ def _compile(src: str) -> str:
     if errs.strip():
         sys.stderr.write(errs + "\n")
     return obj
+
+
+CPP_TESTS = ["test_sdpa_int4"]
+CPP_TEST_DIR = os.path.join(os.path.dirname(HERE), "tests", "cpp")
+
+
+def build_cpp_tests() -> list:
+    """Compile the C++ API tests (tests/cpp/*.cpp) against the library, with
+    an rpath to it, so the GPU box runs them without building."""
+    outs = []
+    for name in CPP_TESTS:
+        src = os.path.join(CPP_TEST_DIR, name + ".cpp")
+        exe = os.path.join(CPP_TEST_DIR, name)
+        cmd = [_hipcc(), "-O2", "-std=c++17", f"-I{INCLUDE}", "-x", "c++", src, "-o", exe,
+               f"-L{HERE}", "-lturboquant_hip", "-Wl,-rpath,$ORIGIN/../../gemma4metal_amd"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stderr}")
+        outs.append(exe)
+    return outs
 
 
 def build(verbose: bool = False) -> str:
@@ -63,6 +85,7 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_cpp_tests()
     if verbose:
         print(f"built {LIB}")
     return LIB
