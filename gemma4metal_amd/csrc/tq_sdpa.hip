@@ -71,29 +71,42 @@ int head_subgroup(int gqa) {
   return 1;
 }
 
-// Keys per workgroup: enough workgroups to fill 256 CUs several times over,
-// never fewer than kMinChunk rows.
-int plan_chunk(int max_len, int64_t groups) {
+// Keys per workgroup: about one workgroup per CU over `groups` (sequence,
+// kv head, head subgroup) groups of max_len keys, never fewer than kMinChunk
+// rows.  A batched (ragged) launch also splits every sequence of max_len into
+// at least min_splits chunks: its sequences differ in length, and a long one
+// in one chunk is the tail of the whole launch.  (Measured on the B=64 ragged
+// workload: 2 beats 1, 4 and 8 -- each split adds a workgroup's fixed
+// prologue / merge cost.)
+int plan_chunk(int max_len, int64_t groups, int min_splits) {
   // never more than kMaxSplits chunks per sequence
   const int64_t floor_c = (static_cast<int64_t>(max_len) + kMaxSplits - 1) / kMaxSplits;
   const int forced = env_int("TQ_SDPA_CHUNK", 0);
   if (forced > 0) return static_cast<int>(std::max<int64_t>(forced, floor_c));
   const int64_t want = (static_cast<int64_t>(max_len) * groups + target_wgs() - 1) / target_wgs();
   int64_t c = (want + kChunkGranule - 1) / kChunkGranule * kChunkGranule;
+  if (min_splits > 1) {
+    const int64_t per = (static_cast<int64_t>(max_len) + min_splits - 1) / min_splits;
+    c = std::min(c, (per + kChunkGranule - 1) / kChunkGranule * kChunkGranule);
+  }
   c = std::max<int64_t>({c, int64_t{kMinChunk}, floor_c});
   return static_cast<int>(std::min<int64_t>(c, 1 << 30));
 }
 
-// Upper bound of ceil(L / plan_chunk(L, groups)) over every L <= max_len
-// (plan_chunk is not monotone in L, the bound is): sizes grids and workspaces.
-int max_splits_bound(int max_len, int64_t groups) {
+// Upper bound of ceil(L / plan_chunk(L, groups, min_splits)) over every
+// L <= max_len (plan_chunk is not monotone in L, the bound is): sizes grids
+// and workspaces.
+int max_splits_bound(int max_len, int64_t groups, int min_splits) {
   if (max_len <= 0) return 1;
   const int forced = env_int("TQ_SDPA_CHUNK", 0);
   if (forced > 0) return std::min((max_len + forced - 1) / forced, kMaxSplits);  // chunk >= ceil(L/kMaxSplits)
   const int64_t by_len = (static_cast<int64_t>(max_len) + kMinChunk - 1) / kMinChunk;
-  const int64_t by_wgs = (target_wgs() + groups - 1) / groups;
+  const int64_t by_wgs = std::max<int64_t>((target_wgs() + groups - 1) / groups, min_splits);
   return static_cast<int>(std::max<int64_t>(1, std::min({by_len, by_wgs, int64_t{kMaxSplits}})));
 }
+
+// Chunks per sequence of max_len a launch of `batch` sequences uses at least.
+int min_splits_for(int batch) { return batch > 1 ? 2 : 1; }
 
 // Workspace: [split counters | (m, l) partials | O partials].  The counter
 // region has a FIXED size at offset 0 so that no call's partials ever overlap
@@ -390,8 +403,8 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
   int eff_len = max_len;
   if (!seq_lens && window > 0) eff_len = std::min(max_len, window);
-  const int chunk = plan_chunk(eff_len, groups);
-  const int max_splits = max_splits_bound(eff_len, groups);
+  const int chunk = plan_chunk(eff_len, groups, min_splits_for(batch));
+  const int max_splits = max_splits_bound(eff_len, groups, min_splits_for(batch));
   const WsLayout wl = ws_layout(batch, Hq, D, max_splits);
   if (max_splits > 1) {
     if (!workspace || ws_bytes < wl.total) {
@@ -450,7 +463,7 @@ extern "C" size_t tq_sdpa_int4_workspace_size(int batch, int num_heads, int num_
   const int gqa = num_heads / num_kv_heads;
   const int G = head_subgroup(gqa);
   const int64_t groups = static_cast<int64_t>(batch) * num_kv_heads * (gqa / G);
-  const int splits = max_splits_bound(max_kv_len, groups);
+  const int splits = max_splits_bound(max_kv_len, groups, min_splits_for(batch));
   return ws_layout(batch, num_heads, head_dim, splits).total;
 }
 
