@@ -188,18 +188,43 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int base0 = t_begin + wv * 32;
   const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
   const int last = t_end - 1;
+
+  // q is loaded first: at kernel start every workgroup issues its K/V stream
+  // at once, and the prologue (which needs only q) should not wait for it.
+  // Then the first iteration's K/V loads go out and stay in flight while
+  // the prologue runs.
+  // (one dword load per element for every q dtype -- no branch around the
+  // load, so the wait before the prologue covers q only, not the K/V loads
+  // issued after it)
+  uint32_t qraw[NE];
+  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = min(static_cast<int>(threadIdx.x) + k * kNT, G * D - 1);
+    const int64_t byte = (qbase + e) * qsz;
+    qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
+    if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Issued unconditionally (a load under a branch makes the compiler drain
+  // every outstanding load at the join): rows are clamped into
+  // [0, max(last, 0)], valid memory even for a wave or split with no keys
+  // (capacity >= 1).
   IterBuf<D> bufA, bufB;
-  if (nit > 0) load_iter<D, G>(bufA, kq_row0, vq_row0, sc_arr, lr, base0, last, m, c);
+  const int safe_last = max(last, 0);
+  load_iter<D, G>(bufA, kq_row0, vq_row0, sc_arr, lr, min(base0, safe_last), safe_last, m, c);
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue: q as 22-bit fixed point per head, B operands via LDS ------
   float qv[NE];
-  {
-    const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
 #pragma unroll
-    for (int k = 0; k < NE; ++k) {
-      const int e = threadIdx.x + k * kNT;
-      qv[k] = e < G * D ? load_any(p.q, p.q_dtype, qbase + e) * p.scale_log2 : 0.0f;
-    }
+  for (int k = 0; k < NE; ++k) {
+    const uint32_t w = qraw[k];
+    const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
+                    : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
+                                          : __uint_as_float(w << 16);
+    qv[k] = threadIdx.x + k * kNT < G * D ? f * p.scale_log2 : 0.0f;
   }
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
@@ -399,17 +424,15 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     load_iter<D, G>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c);
   };
 
-  if (nit > 0) {
-    for (int it = 0; it < nit; it += 2) {
-      load_next(bufB, base0 + (it + 1) * kIter);
-      __builtin_amdgcn_sched_barrier(0);
-      process(bufA, base0 + it * kIter);
-      __builtin_amdgcn_sched_barrier(0);
-      load_next(bufA, base0 + (it + 2) * kIter);
-      __builtin_amdgcn_sched_barrier(0);
-      if (it + 1 < nit) process(bufB, base0 + (it + 1) * kIter);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  for (int it = 0; it < nit; it += 2) {
+    load_next(bufB, base0 + (it + 1) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    process(bufA, base0 + it * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    load_next(bufA, base0 + (it + 2) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < nit) process(bufB, base0 + (it + 1) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // ---- per-wave result into the finalisation arena --------------------------
