@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8, help="distinct KV sets rotated")
     ap.add_argument("--workload", default="ctx32k",
-                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar"])
+                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar", "global"])
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -234,6 +234,28 @@ def main():
 
     if args.workload == "polar":
         bench_polar(args, torch, gen)
+        return
+
+    if args.workload == "global":
+        # Gemma global-attention layer shape (engine/gemma4_multilayer.cpp:3,49-51):
+        # Hq 32, Hkv 4 (GQA 8), D 512, no window
+        Hg, Hkvg, Dg, L = 32, 4, 512, args.ctx
+        nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkvg * L * 576)))
+        sets = [gen_cache(tq, torch, Hkvg, L, Dg, gen) for _ in range(nsets)]
+        qs = [gen_q(torch, (Hg, Dg), gen) for _ in range(nsets)]
+        out = torch.empty((Hg, Dg), dtype=torch.float32, device="cuda")
+        nbytes = O.decode_bytes(Hg, Hkvg, Dg, L)
+        ms_step, _, _ = time_launches(torch, lambda i: tq.sdpa_int4(
+            qs[i % nsets], *sets[i % nsets], Hg // Hkvg, 1.0, 0, out=out), args.steps, args.warmup)
+        gbs = nbytes / (ms_step * 1e-3) / 1e9
+        emit({"metric": "int4-KV decode SDPA GB/s, Gemma global layer (D 512, GQA 8)",
+              "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+              "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+              "us_per_layer": round(ms_step * 1e3, 2), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
+              "config": {"workload": f"sdpa_int4 Hq={Hg} Hkv={Hkvg} D={Dg} L={L} W=0 (global layer)",
+                         "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"}}, args)
         return
 
     if args.workload == "sliding50":
