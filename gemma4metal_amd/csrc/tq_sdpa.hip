@@ -398,7 +398,18 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
                "%s: k_quant / v_quant must be 16-byte aligned", fn);
   TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
 
-  const int G = head_subgroup(gqa);
+  // Matrix-core kernel when it serves (D, G); the VALU kernel otherwise or
+  // when TQ_SDPA_IMPL=valu forces it.  At D = 512 the matrix-core kernel
+  // takes at most 2 query heads per workgroup (2 heads x 8 quant groups fill
+  // its 16 columns): the head subgroups of one kv head then read the same
+  // K/V, concurrently and on one XCD (splits are a multiple of 8 at long
+  // contexts), so the repeats are served mostly from L2.  (The workspace
+  // bound of tq_sdpa_int4_workspace_size, planned with the largest subgroup,
+  // covers this: more groups never means more splits.)
+  const char* impl = std::getenv("TQ_SDPA_IMPL");
+  const bool try_mfma = !(impl && std::string(impl) == "valu");
+  int G = head_subgroup(gqa);
+  if (try_mfma && D == 512 && sb_dtype == TQ_F16) G = gqa % 2 == 0 ? 2 : 1;
   const int n_sub = gqa / G;
   const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
   int eff_len = max_len;
@@ -438,10 +449,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
 
   dim3 grid(max_splits, Hkv * n_sub, batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Matrix-core kernel when it serves (D, G); the VALU kernel otherwise or
-  // when TQ_SDPA_IMPL=valu forces it.
-  const char* impl = std::getenv("TQ_SDPA_IMPL");
-  if (!(impl && std::string(impl) == "valu")) {
+  if (try_mfma) {
     const int r = launch_sdpa_mfma(p, D, G, sb_dtype, grid, s);
     if (r >= 0) return r;
   }

@@ -33,7 +33,8 @@
 namespace tq {
 namespace {
 
-// Waves per workgroup: 8 = two waves per SIMD at one workgroup per CU.
+// Waves per workgroup: 8 = two waves per SIMD at one workgroup per CU
+// (D = 512: 4, one wave per SIMD).
 constexpr int kMfmaWaves = 8;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -52,7 +53,7 @@ struct MGeom {
   static constexpr int VM = 8 * VW;     // f16 MFMAs per iteration (= D/16)
   static constexpr int SCW = NG / 2;    // 32-bit words of one key's scales
   static_assert(COLS <= 16, "more than 16 (head, group) columns");
-  static_assert(D == 128 || D == 256, "D");
+  static_assert(D == 128 || D == 256 || D == 512, "D");
 };
 
 template <int D>
@@ -97,7 +98,10 @@ __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t off = static_cast<uint32_t>(min(lr.v[j], lim)) * RB + m * Gm::VW * 4;
-    if constexpr (Gm::VW == 2) {
+    if constexpr (Gm::VW == 4) {
+      const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off));
+      B.vw[j][0] = u.x; B.vw[j][1] = u.y; B.vw[j][2] = u.z; B.vw[j][3] = u.w;
+    } else if constexpr (Gm::VW == 2) {
       const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vb + off));
       B.vw[j][0] = u.x; B.vw[j][1] = u.y;
     } else {
@@ -107,7 +111,10 @@ __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const uint32_t off = static_cast<uint32_t>(min(lr.s[e], lim)) * (Gm::SCW * 4);
-    if constexpr (Gm::SCW == 2) {
+    if constexpr (Gm::SCW == 4) {
+      const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sb + off));
+      B.sc[e][0] = u.x; B.sc[e][1] = u.y; B.sc[e][2] = u.z; B.sc[e][3] = u.w;
+    } else if constexpr (Gm::SCW == 2) {
       const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(sb + off));
       B.sc[e][0] = u.x; B.sc[e][1] = u.y;
     } else {
@@ -135,8 +142,11 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// D = 512 needs ~300 registers per lane (two 72-word buffers and 32 V
+// accumulator tiles): one wave per SIMD (VGPRs + AGPRs), 4-wave workgroups.
 template <int D, int G, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void sdpa_int4_mfma_kernel(SdpaParams p) {
   constexpr int kNT = NW * 64;       // threads per workgroup
   constexpr int kIter = 32 * NW;     // keys per workgroup iteration
@@ -468,7 +478,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
 template <int D, int G>
 int launch_dg(const SdpaParams& p, dim3 grid, hipStream_t s) {
-  constexpr int NW = kMfmaWaves;
+  constexpr int NW = D == 512 ? 4 : kMfmaWaves;
   sdpa_int4_mfma_kernel<D, G, NW><<<grid, NW * 64, 0, s>>>(p);
   TQ_CHECK_LAUNCH("sdpa_int4_mfma_kernel");
   return TQ_OK;
@@ -483,6 +493,9 @@ int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
     if (G == 1) return launch_dg<256, 1>(p, grid, stream);
     if (G == 2) return launch_dg<256, 2>(p, grid, stream);
     if (G == 4) return launch_dg<256, 4>(p, grid, stream);
+  } else if (D == 512) {
+    if (G == 1) return launch_dg<512, 1>(p, grid, stream);
+    if (G == 2) return launch_dg<512, 2>(p, grid, stream);
   } else if (D == 128) {
     if (G == 1) return launch_dg<128, 1>(p, grid, stream);
     if (G == 2) return launch_dg<128, 2>(p, grid, stream);
