@@ -33,8 +33,7 @@
 namespace tq {
 namespace {
 
-// Waves per workgroup: 8 = two waves per SIMD at one workgroup per CU
-// (D = 512: 4, one wave per SIMD).
+// Waves per workgroup: 8 = two waves per SIMD at one workgroup per CU.
 constexpr int kMfmaWaves = 8;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -50,7 +49,12 @@ struct MGeom {
   static constexpr int KW = D / 32;     // K words per lane per key (D/8 bytes)
   static constexpr int KM = D / 64;     // int8 MFMAs per 16-key tile (2 words each)
   static constexpr int VW = D / 128;    // V words per lane per key
-  static constexpr int VM = 8 * VW;     // f16 MFMAs per iteration (= D/16)
+  // V split: at D = 512 a pair of waves takes the same keys, each wave
+  // accumulating half of every lane's V words (registers for two buffers
+  // and the accumulators then fit two waves per SIMD)
+  static constexpr int VS = D == 512 ? 2 : 1;
+  static constexpr int VWH = VW / VS;   // V words per lane per key of one wave
+  static constexpr int VM = 8 * VWH;    // f16 accumulator tiles of one wave
   static constexpr int SCW = NG / 2;    // 32-bit words of one key's scales
   static_assert(COLS <= 16, "more than 16 (head, group) columns");
   static_assert(D == 128 || D == 256 || D == 512, "D");
@@ -59,7 +63,7 @@ struct MGeom {
 template <int D>
 struct IterBuf {
   uint32_t kw[2][D / 32];   // [tile][word] K slice of key (t0 + 16*tile + m)
-  uint32_t vw[8][D / 128];  // [slot][word]  V words of key(slot)
+  uint32_t vw[8][D / 128 / (D == 512 ? 2 : 1)];  // [slot][word] this wave's V words of key(slot)
   uint32_t sc[2][D / 128];  // scales of keys (t0 + 2k, t0 + 2k + 1) of array l/16
 };
 
@@ -79,7 +83,8 @@ struct LaneRows {
 template <int D, int G>
 __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0,
                                           const uint32_t* vq_row0, const uint32_t* sc_arr,
-                                          const LaneRows& lr, int t0, int last, int m, int c) {
+                                          const LaneRows& lr, int t0, int last, int m, int c,
+                                          int vhalf) {
   using Gm = MGeom<D, G>;
   constexpr uint32_t RB = D / 2;  // bytes per packed row
   const int lim = last - t0;      // uniform; >= 0 for every issued iteration
@@ -97,11 +102,12 @@ __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t off = static_cast<uint32_t>(min(lr.v[j], lim)) * RB + m * Gm::VW * 4;
-    if constexpr (Gm::VW == 4) {
+    const uint32_t off = static_cast<uint32_t>(min(lr.v[j], lim)) * RB +
+                         (m * Gm::VW + vhalf * Gm::VWH) * 4;
+    if constexpr (Gm::VWH == 4) {
       const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off));
       B.vw[j][0] = u.x; B.vw[j][1] = u.y; B.vw[j][2] = u.z; B.vw[j][3] = u.w;
-    } else if constexpr (Gm::VW == 2) {
+    } else if constexpr (Gm::VWH == 2) {
       const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vb + off));
       B.vw[j][0] = u.x; B.vw[j][1] = u.y;
     } else {
@@ -142,16 +148,18 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
-// D = 512 needs ~300 registers per lane (two 72-word buffers and 32 V
-// accumulator tiles): one wave per SIMD (VGPRs + AGPRs), 4-wave workgroups.
+// D = 512: 4-wave workgroups at one wave per SIMD (VGPRs + AGPRs for the
+// doubled K buffers and scales).
 template <int D, int G, int NW>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void sdpa_int4_mfma_kernel(SdpaParams p) {
   constexpr int kNT = NW * 64;       // threads per workgroup
-  constexpr int kIter = 32 * NW;     // keys per workgroup iteration
+  constexpr int kIter = 32 * (NW / MGeom<D, G>::VS);  // keys per workgroup iteration
   using Gm = MGeom<D, G>;
   constexpr int NG = Gm::NG, COLS = Gm::COLS, KM = Gm::KM, VW = Gm::VW, VM = Gm::VM;
+  constexpr int VS = Gm::VS, VWH = Gm::VWH;
+  constexpr int NWK = NW / VS;       // waves per key stream
   constexpr int RW = D / 8;
   constexpr int NE = (G * D + kNT - 1) / kNT;  // q elements per thread
 
@@ -195,7 +203,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   lr.s[1] = 2 * k16 + 1;
 
   const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const int base0 = t_begin + wv * 32;
+  // wave wv streams keys with the NWK waves of its V half (wv / NWK)
+  const int vhalf = wv / NWK;
+  const int base0 = t_begin + (wv - vhalf * NWK) * 32;
   const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
   const int last = t_end - 1;
 
@@ -223,7 +233,8 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // (capacity >= 1).
   IterBuf<D> bufA, bufB;
   const int safe_last = max(last, 0);
-  load_iter<D, G>(bufA, kq_row0, vq_row0, sc_arr, lr, min(base0, safe_last), safe_last, m, c);
+  load_iter<D, G>(bufA, kq_row0, vq_row0, sc_arr, lr, min(base0, safe_last), safe_last, m, c,
+                  vhalf);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue: q as 22-bit fixed point per head, B operands via LDS ------
@@ -403,7 +414,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
     // P . V on the f16 matrix cores: A = (1024 + nibble) of 16 dims x 32 keys
 #pragma unroll
-    for (int s = 0; s < VW; ++s) {
+    for (int s = 0; s < VWH; ++s) {
 #pragma unroll
       for (int by = 0; by < 4; ++by) {
         const uint32_t sel = static_cast<uint32_t>(by) | (0x0Cu << 8) |
@@ -431,7 +442,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   };
 
   auto load_next = [&](IterBuf<D>& B, int t0) {
-    load_iter<D, G>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c);
+    load_iter<D, G>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c, vhalf);
   };
 
   for (int it = 0; it < nit; it += 2) {
@@ -456,21 +467,31 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   bacc += shfl_xor_f(bacc, 16);
   bacc += shfl_xor_f(bacc, 32);
   if (col_used) {
+    // a wave's arena slot covers every dim: its own V words' dims get the
+    // result, the other V half's dims zero; only V half 0 counts the
+    // denominator (both halves scored the same keys)
 #pragma unroll
-    for (int s = 0; s < VW; ++s)
+    for (int sg = 0; sg < VW; ++sg)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int dim = 8 * (VW * (4 * c + i) + s) + j;
+          const int dim = 8 * (VW * (4 * c + i) + sg) + j;
           if ((dim >> 6) == gn) {
-            const float off = (j & 1) ? 64.0f : 1024.0f;
-            Fin::o(arena, wave, hn)[dim] = (cv[8 * s + j][i] - off * wsum) + bacc;
+            const int s = sg - vhalf * VWH;  // this wave's word index, if owned
+            float v = 0.0f;
+#pragma unroll
+            for (int so = 0; so < VWH; ++so)
+              if (so == s) {
+                const float off = (j & 1) ? 64.0f : 1024.0f;
+                v = (cv[8 * so + j][i] - off * wsum) + bacc;
+              }
+            Fin::o(arena, wave, hn)[dim] = v;
           }
         }
     if (gn == 0 && c == 0) {
       Fin::m(arena, wave)[hn] = m_run;
-      Fin::l(arena, wave)[hn] = l_sum;
+      Fin::l(arena, wave)[hn] = vhalf == 0 ? l_sum : 0.0f;
     }
   }
   Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
