@@ -693,11 +693,20 @@ struct P7Keys {
 //     the top-down decode per lookup (levels 7-6, 5-4, 3-2).
 template <int G>
 struct P7Tables {
-  float t1[G][64][16];
+  float t1[G][64][16];  // rows rotated, see p7_t1_row
   float tq[G][16][256];
   float4 t2[64];
   float U[G];
 };
+
+// LDS row of level-1 row 16 qt + jj (pair jj of quarter qt): the rows are
+// rotated within each group of four, to 16 qt + (jj & ~3) + ((jj + qt) & 3).
+// The four lanes of a key read row jj of their quarters in one instruction;
+// the rotation puts those rows into four different 16-bank groups.
+__device__ __forceinline__ int p7_t1_row(int row) {
+  const int qt = row >> 4, jj = row & 15;
+  return (row & ~15) | (jj & ~3) | ((jj + qt) & 3);
+}
 
 // Copies the query tables of heads h0 .. h0+G-1 into LDS and builds the
 // combined two-level table t2[kp | k0 << 2 | k1 << 4] = (cos_p cos_0,
@@ -711,7 +720,7 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
   for (int i = threadIdx.x; i < G * kVec; i += NT) {
     const int g = i / kVec, r = i - (i / kVec) * kVec;
     const float4 v = reinterpret_cast<const float4*>(k.qtab + static_cast<int64_t>(h0 + g) * kP7QTab)[r];
-    if (r < 256) reinterpret_cast<float4*>(&T.t1[g][0][0])[r] = v;
+    if (r < 256) reinterpret_cast<float4*>(&T.t1[g][0][0])[p7_t1_row(r >> 2) * 4 + (r & 3)] = v;
     else if (r < 1280) reinterpret_cast<float4*>(&T.tq[g][0][0])[r - 256] = v;
     else if (r == 1280) T.U[g] = v.x;
   }
@@ -794,17 +803,35 @@ struct P7Quarter {
   uint32_t nrm;
 };
 
-__device__ __forceinline__ void load_p7_quarter(const P7Keys& k, int64_t row, int qt, P7Quarter& Q) {
-  const uint32_t* a = k.angles + row * kP7Words;
-  const u32x2v l1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(a + 2 * qt));
+// Row pointers of the key arrays at a wave-uniform first row; the lanes add
+// 32-bit row offsets (scalar base + vector offset addressing).
+struct P7Rows {
+  const uint32_t* ang;
+  const uint32_t* nrm;
+  const uint32_t* qjl;
+};
+
+__device__ __forceinline__ P7Rows p7_rows(const P7Keys& k, int64_t row0) {
+  return P7Rows{k.angles + row0 * kP7Words, k.norms + row0, k.qjl + row0 * 4};
+}
+
+template <typename T>
+__device__ __forceinline__ T nt_at(const void* base, uint32_t byte_off) {
+  return __builtin_nontemporal_load(
+      reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off));
+}
+
+__device__ __forceinline__ void load_p7_quarter(const P7Rows& R, uint32_t off, int qt, P7Quarter& Q) {
+  const uint32_t a = off * (kP7Words * 4);
+  const u32x2v l1 = nt_at<u32x2v>(R.ang, a + 8 * qt);
   Q.l1[0] = l1.x;
   Q.l1[1] = l1.y;
-  Q.l2 = __builtin_nontemporal_load(a + 8 + (qt >> 1));
-  const u32x2v hi = __builtin_nontemporal_load(reinterpret_cast<const u32x2v*>(a + 10));
+  Q.l2 = nt_at<uint32_t>(R.ang, a + 32 + 4 * (qt >> 1));
+  const u32x2v hi = nt_at<u32x2v>(R.ang, a + 40);
   Q.w10 = hi.x;
   Q.w11 = hi.y;
-  Q.qj = __builtin_nontemporal_load(k.qjl + row * 4 + qt);
-  Q.nrm = __builtin_nontemporal_load(k.norms + row);
+  Q.qj = nt_at<uint32_t>(R.qjl, off * 16 + 4 * qt);
+  Q.nrm = nt_at<uint32_t>(R.nrm, off * 4);
 }
 
 __device__ __forceinline__ float pick4(const float4& v, int i) {
@@ -830,16 +857,25 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
     qa[g] = 0.0f;
     acc[g] = 0.0f;
   }
+  // byte addresses: lane base + (index << 2), constant parts in the
+  // instruction's offset field
+  const char* tqb = reinterpret_cast<const char*>(&T.tq[0][0][0]) + qt * 4096;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    const uint32_t byte = (Q.qj >> (8 * b)) & 255u;
+    const uint32_t byte = __builtin_amdgcn_ubfe(Q.qj, 8 * b, 8);
 #pragma unroll
-    for (int g = 0; g < G; ++g) qa[g] += T.tq[g][4 * qt + b][byte];
+    for (int g = 0; g < G; ++g)
+      qa[g] += *reinterpret_cast<const float*>(tqb + g * 16384 + b * 1024 + (byte << 2));
   }
   const float R = h2f_lo(Q.nrm), rn = h2f_hi(Q.nrm);
   const float r5 = R * pick4(ta, qt);
   const float r3[4] = {r5 * tb.x, r5 * tb.y, r5 * tb.z, r5 * tb.w};
-  const float* t1 = &T.t1[0][16 * qt][0];
+  // rotated level-1 rows (p7_t1_row): row jj of quarter qt is at
+  // 16 qt + (jj & ~3) + ((jj + qt) & 3)
+  const char* t1b = reinterpret_cast<const char*>(&T.t1[0][0][0]) + qt * 1024;
+  uint32_t rot[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) rot[e] = static_cast<uint32_t>((e + qt) & 3) * 64;
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
     const float r1[4] = {r3[ii] * tc[ii].x, r3[ii] * tc[ii].y, r3[ii] * tc[ii].z, r3[ii] * tc[ii].w};
@@ -847,9 +883,11 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int jj = 4 * ii + e;  // level-1 pair 16 qt + jj
-      const uint32_t nib = (word >> (4 * (jj % 8))) & 15u;
+      const uint32_t nib = __builtin_amdgcn_ubfe(word, 4 * (jj % 8), 4);
+      const char* row = t1b + ii * 256 + rot[e] + (nib << 2);
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = fmaf(r1[e], t1[g * 1024 + jj * 16 + nib], acc[g]);
+      for (int g = 0; g < G; ++g)
+        acc[g] = fmaf(r1[e], *reinterpret_cast<const float*>(row + g * 4096), acc[g]);
     }
   }
   const float cr = kQjlCoef * rn;
@@ -882,8 +920,11 @@ __global__ __launch_bounds__(256) void polar7_score_kernel(P7Keys k, int n, int 
   const int last = n - 1;
   const int64_t rowbase = static_cast<int64_t>(kvh) * cap;
   const int npass = min(16, (n - blockIdx.x * 1024 + 63) / 64);
+  // rows of this workgroup: rowbase + blockIdx.x * 1024 + (0 .. lim)
+  const P7Rows R = p7_rows(k, rowbase + blockIdx.x * 1024);
+  const uint32_t lim = static_cast<uint32_t>(last - blockIdx.x * 1024);
   P7Quarter A, B;
-  load_p7_quarter(k, rowbase + min(t0, last), qt, A);
+  load_p7_quarter(R, min(static_cast<uint32_t>(key), lim), qt, A);
   load_p7_tables<G, 256>(T, k, h0);
   auto pass = [&](const P7Quarter& Q, int r) {
     float s[G];
@@ -898,9 +939,9 @@ __global__ __launch_bounds__(256) void polar7_score_kernel(P7Keys k, int n, int 
     }
   };
   for (int r = 0; r < npass; r += 2) {
-    load_p7_quarter(k, rowbase + min(t0 + 64 * (r + 1), last), qt, B);
+    load_p7_quarter(R, min(static_cast<uint32_t>(key + 64 * (r + 1)), lim), qt, B);
     pass(A, r);
-    load_p7_quarter(k, rowbase + min(t0 + 64 * (r + 2), last), qt, A);
+    load_p7_quarter(R, min(static_cast<uint32_t>(key + 64 * (r + 2)), lim), qt, A);
     if (r + 1 < npass) pass(B, r + 1);
   }
 }
@@ -916,77 +957,115 @@ __device__ __forceinline__ float2 sb_pair<float>(const uint32_t* w) {
   return make_float2(__uint_as_float(w[0]), __uint_as_float(w[1]));
 }
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// K slot of tile key t (0..63) in the P.V operands: key 32 kb + 4 j + c is
+// slot 32 kb + 8 c + j (lane group c of the B operand holds slots 8c .. 8c+7).
+__device__ __forceinline__ int p7_slot(int t) { return (t & 32) | ((t & 3) << 3) | ((t >> 2) & 7); }
+
 // configs[4] attention: polar7 + QJL scores, softmax, int4 V (group 64,
-// scale/bias SB), split-K.  Per 64-key tile of a wave: four lanes per key
-// for the scores (4 sub-tiles of 16 keys); the weights and the V scale/bias
-// of key `lane` go through LDS; then
-// 16 steps of 4 keys x 16 words for V (lane: key 4*step + lane/16, dims
-// 8*(lane%16) .. +7).  Key words are loaded one tile ahead; the V words of a
-// tile are issued before its scores are computed.
+// scale/bias SB), split-K.  Per 64-key tile of a wave:
+//  - scores: four lanes per key (quarter qt = lane & 3) over four sub-tiles
+//    of 16 keys; the key words are loaded one tile ahead, the V words of a
+//    tile before its scores (which hide their latency);
+//  - the weights p and the tile's V scale / bias go to LDS in K-slot order;
+//  - P.V on v_mfma_f32_16x16x32_bf16, two blocks of 32 keys: A = (128 +
+//    nibble) as bf16 for 16 V words x 32 keys (lane: word lane % 16 of keys
+//    32 kb + 4 j + lane / 16, one v_perm + and-or per two nibbles), B = the
+//    bf16 hi / lo split of p * s_v (~16 bits) in columns (head, quant group).
+//    bf16 keeps fp32's exponent range, so no scale of V can overflow it.
+//    The 128 offset (128 * sum(hi + lo)) and the bias term sum(p * b_v) are
+//    accumulated per column and removed at the end.
 template <int G, typename SB>
-__global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
   constexpr int NW = 4, D = 128;
   __shared__ P7Tables<G> T;
   using Fin = Finalize<G, D, NW>;
   __shared__ float arena[Fin::kArena];
-  __shared__ float p_lds[NW][G][64];
-  __shared__ float2 sb_lds[NW][64][2];  // [wave][key][group] = (scale, bias)
+  __shared__ float p_lds[NW][G][64];   // [wave][head][slot]
+  __shared__ float sv_lds[NW][2][64];  // [wave][quant group][slot] V scale
+  __shared__ float bv_lds[NW][2][64];  // V bias
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hy = blockIdx.y, split = blockIdx.x;
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
   const int h0 = kvh * p.gqa + sub * G;
   const SplitRange rg = split_range(p, 0, split);
   if (split >= rg.S) return;
-  const int wd = lane & 15, kg = lane >> 4, gq = wd >> 3;
   const int64_t rowbase = static_cast<int64_t>(kvh) * p.cap;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int base0 = rg.t_begin + wv * 64;
   const int last = rg.t_end - 1;
   const int ntile = base0 < rg.t_end ? (rg.t_end - base0 + NW * 64 - 1) / (NW * 64) : 0;
   constexpr int SBW = sizeof(SB) / 2;  // words of one row's two scales (or biases)
-  // scoring layout: four lanes per key (quarter qt = lane & 3), the 64 keys
-  // of a tile as 4 sub-tiles u of 16 keys: key 16u + (lane >> 2)
-  const int qt = lane & 3, kq = lane >> 2;
-  P7Quarter keyA[4], keyB[4];
-  auto load_keys = [&](P7Quarter* Q, int tb) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) load_p7_quarter(k, rowbase + min(tb + 16 * u + kq, last), qt, Q[u]);
+  const int qt = lane & 3, kq = lane >> 2;  // scoring: quarter, key of the sub-tile
+  const int vm = lane & 15, vc = lane >> 4;  // P.V: V word / B column, K-slot group
+  const int cg = (vm >> 1) % G, cgr = vm & 1;  // this lane's B column (head, quant group)
+  const int my_slot = p7_slot(lane);
+
+  // Key words of sub-tile u (keys 16 u + (lane >> 2)) of the current tile;
+  // once scored, each sub-tile's registers receive the next tile's words.
+  P7Quarter key[4];
+  auto load_sub = [&](P7Quarter& Q, int tb, int u) {
+    const P7Rows R = p7_rows(k, rowbase + tb);
+    load_p7_quarter(R, min(static_cast<uint32_t>(16 * u + kq), static_cast<uint32_t>(last - tb)), qt, Q);
   };
-  if (ntile > 0) load_keys(keyA, base0);
+  if (ntile > 0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_sub(key[u], base0, u);
+  }
   load_p7_tables<G, NW * 64>(T, k, h0);
 
-  float m_run[G], l_run[G], acc[G][8], accb[G];
+  float m_run[G], l_run[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m_run[g] = -INFINITY;
     l_run[g] = 0.0f;
-    accb[g] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
   }
+  float wsum = 0.0f, bacc = 0.0f;  // this lane's column: sum(hi + lo), sum(p * b_v)
+  v4f cv[8];                       // [2 * byte + nibble half]
+#pragma unroll
+  for (int f = 0; f < 8; ++f) cv[f] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  // bf16 magic of (128 + nibble), in a VGPR so each A word is one and-or
+  uint32_t magic = 0x43004300u;
+  asm volatile("" : "+v"(magic));
 
-  auto process = [&](const P7Quarter* K, int tb) {
-    // V words of the tile (consumed after the scores, which hide their latency)
-    const int64_t row = rowbase + min(tb + lane, last);
-    uint32_t vsw[SBW], vbw[SBW], vw[16];
+  // tile at tb; tn = first key of the next tile (clamped into the split)
+  auto process = [&](int tb, int tn) {
+    const uint32_t lim = static_cast<uint32_t>(last - tb);
+    const uint32_t* vrow = p.vq + (rowbase + tb) * 16;
+    uint32_t vw[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t key = min(static_cast<uint32_t>(32 * kb + 4 * j + vc), lim);
+        vw[kb][j] = nt_at<uint32_t>(vrow, key * 64 + vm * 4);
+      }
+    const uint32_t kl = min(static_cast<uint32_t>(lane), lim);
+    const void* vsrow = static_cast<const uint32_t*>(p.vs) + (rowbase + tb) * SBW;
+    const void* vbrow = static_cast<const uint32_t*>(p.vb) + (rowbase + tb) * SBW;
+    uint32_t vsw[SBW], vbw[SBW];
 #pragma unroll
     for (int i = 0; i < SBW; ++i) {
-      vsw[i] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p.vs) + row * SBW + i);
-      vbw[i] = __builtin_nontemporal_load(static_cast<const uint32_t*>(p.vb) + row * SBW + i);
+      vsw[i] = nt_at<uint32_t>(vsrow, (kl * SBW + i) * 4);
+      vbw[i] = nt_at<uint32_t>(vbrow, (kl * SBW + i) * 4);
     }
-#pragma unroll
-    for (int st = 0; st < 16; ++st)
-      vw[st] = __builtin_nontemporal_load(p.vq + (rowbase + min(tb + 4 * st + kg, last)) * 16 + wd);
     float s[4][G];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      p7_quarter_score<G>(T, K[u], qt, p.scale_log2, s[u]);
+      p7_quarter_score<G>(T, key[u], qt, p.scale_log2, s[u]);
+      load_sub(key[u], tn, u);
       quarter_sum<G>(s[u]);
       const bool valid = tb + 16 * u + kq < rg.t_end;
 #pragma unroll
       for (int g = 0; g < G; ++g) s[u][g] = valid ? s[u][g] : -INFINITY;
     }
     __builtin_amdgcn_sched_barrier(0);
+    // online softmax (log2 domain); a raised max rescales this lane's column
+    float fac = 1.0f;
+    bool raised = false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float mt = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
@@ -994,74 +1073,106 @@ __global__ __launch_bounds__(256) void polar7_sdpa_kernel(SdpaParams p, P7Keys k
       if (m_new > m_run[g]) {  // wave-uniform
         const float f = merge_factor(m_run[g], m_new);
         l_run[g] *= f;
-        accb[g] *= f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] *= f;
+        fac = cg == g ? f : fac;
         m_run[g] = m_new;
+        raised = true;
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const float pw = s[u][g] == -INFINITY ? 0.0f : fast_exp2(s[u][g] - m_run[g]);
         if (qt == 0) {
           l_run[g] += pw;
-          p_lds[wave][g][16 * u + kq] = pw;
+          p_lds[wave][g][p7_slot(16 * u + kq)] = pw;
         }
       }
     }
+    if (raised) {
+      wsum *= fac;
+      bacc *= fac;
+#pragma unroll
+      for (int f = 0; f < 8; ++f) cv[f] *= fac;
+    }
     const float2 sc2 = sb_pair<SB>(vsw), bi2 = sb_pair<SB>(vbw);
-    sb_lds[wave][lane][0] = make_float2(sc2.x, bi2.x);
-    sb_lds[wave][lane][1] = make_float2(sc2.y, bi2.y);
+    sv_lds[wave][0][my_slot] = sc2.x;
+    sv_lds[wave][1][my_slot] = sc2.y;
+    bv_lds[wave][0][my_slot] = bi2.x;
+    bv_lds[wave][1][my_slot] = bi2.y;
     wave_lds_sync();
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const int kk = 4 * st + kg;
-      const float2 sbv = sb_lds[wave][kk][gq];
-      const uint32_t wv4 = vw[st];
-      const uint32_t lo = wv4 & 0x0F0F0F0Fu, hi = (wv4 >> 4) & 0x0F0F0F0Fu;
-      float nv[8];
+    for (int kb = 0; kb < 2; ++kb) {
+      const int s0 = 32 * kb + 8 * vc;
+      const float4 pa = *reinterpret_cast<const float4*>(&p_lds[wave][cg][s0]);
+      const float4 pb = *reinterpret_cast<const float4*>(&p_lds[wave][cg][s0 + 4]);
+      const float4 sa = *reinterpret_cast<const float4*>(&sv_lds[wave][cgr][s0]);
+      const float4 sb = *reinterpret_cast<const float4*>(&sv_lds[wave][cgr][s0 + 4]);
+      const float4 ba = *reinterpret_cast<const float4*>(&bv_lds[wave][cgr][s0]);
+      const float4 bb = *reinterpret_cast<const float4*>(&bv_lds[wave][cgr][s0 + 4]);
+      const float pj[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      const float sj[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+      const float bj[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+      __bf16 hi[8], lo[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        nv[2 * i] = static_cast<float>((lo >> (8 * i)) & 0xFFu);
-        nv[2 * i + 1] = static_cast<float>((hi >> (8 * i)) & 0xFFu);
+      for (int j = 0; j < 8; ++j) {
+        const float w = pj[j] * sj[j];
+        hi[j] = static_cast<__bf16>(w);
+        const float hf = static_cast<float>(hi[j]);
+        lo[j] = static_cast<__bf16>(w - hf);
+        wsum += hf + static_cast<float>(lo[j]);
+        bacc = fmaf(pj[j], bj[j], bacc);
       }
+      const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+      const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pg = p_lds[wave][g][kk];
-        const float ps = pg * sbv.x;
+      for (int by = 0; by < 4; ++by) {
+        // byte `by` of the words of slots 2r, 2r+1 -> the two 16-bit halves
+        const uint32_t sel = static_cast<uint32_t>(by) | (0x0Cu << 8) |
+                             (static_cast<uint32_t>(4 + by) << 16) | (0x0Cu << 24);
+        uint32_t alo[4], ahi[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(ps, nv[j], acc[g][j]);
-        accb[g] = fmaf(pg, sbv.y, accb[g]);
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t x = __builtin_amdgcn_perm(vw[kb][2 * r + 1], vw[kb][2 * r], sel);
+          alo[r] = (x & 0x000F000Fu) | magic;
+          ahi[r] = ((x >> 4) & 0x000F000Fu) | magic;
+        }
+        const v8bf a_lo = __builtin_bit_cast(v8bf, u32x4v{alo[0], alo[1], alo[2], alo[3]});
+        const v8bf a_hi = __builtin_bit_cast(v8bf, u32x4v{ahi[0], ahi[1], ahi[2], ahi[3]});
+        cv[2 * by] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, bhi, cv[2 * by], 0, 0, 0);
+        cv[2 * by + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, bhi, cv[2 * by + 1], 0, 0, 0);
+        cv[2 * by] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, blo, cv[2 * by], 0, 0, 0);
+        cv[2 * by + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, blo, cv[2 * by + 1], 0, 0, 0);
       }
     }
     wave_lds_sync();
   };
 
-  for (int it = 0; it < ntile; it += 2) {
-    load_keys(keyB, min(base0 + (it + 1) * NW * 64, last));
-    process(keyA, base0 + it * NW * 64);
-    load_keys(keyA, min(base0 + (it + 2) * NW * 64, last));
-    if (it + 1 < ntile) process(keyB, base0 + (it + 1) * NW * 64);
+  for (int it = 0; it < ntile; ++it) {
+    const int tb = base0 + it * NW * 64;
+    process(tb, min(tb + NW * 64, last));
   }
 
-  // sum the four key groups of each dimension slice, then one lane per slice
-  // writes its 8 dims (the bias term belongs to the slice's quant group)
+  // columns: sum the four K-slot groups; lane (vm, vc) holds V words
+  // 4 vc + i (dims 8 (4 vc + i) + 2 byte + half) of column vm, and the words
+  // of quant group cgr are those with vc >> 1 == cgr
+  wsum += shfl_xor_f(wsum, 16);
+  wsum += shfl_xor_f(wsum, 32);
+  bacc += shfl_xor_f(bacc, 16);
+  bacc += shfl_xor_f(bacc, 32);
+  float ls[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < G; ++g) ls[g] = wave_sum_f(l_run[g]);
+  if (vm < 2 * G && (vc >> 1) == cgr) {
+    float* o = Fin::o(arena, wave, cg);
+    const float off = bacc - 128.0f * wsum;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      acc[g][j] += shfl_xor_f(acc[g][j], 16);
-      acc[g][j] += shfl_xor_f(acc[g][j], 32);
-    }
-    accb[g] += shfl_xor_f(accb[g], 16);
-    accb[g] += shfl_xor_f(accb[g], 32);
-    const float ls = wave_sum_f(l_run[g]);
-    if (lane < 16) {
+    for (int f = 0; f < 8; ++f)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Fin::o(arena, wave, g)[8 * lane + j] = acc[g][j] + accb[g];
-    }
-    if (lane == 0) {
+      for (int i = 0; i < 4; ++i) o[8 * (4 * vc + i) + f] = cv[f][i] + off;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
       Fin::m(arena, wave)[g] = m_run[g];
-      Fin::l(arena, wave)[g] = ls;
+      Fin::l(arena, wave)[g] = ls[g];
     }
   }
   Fin::run(p, arena, h0, rg.S, split, hy);
