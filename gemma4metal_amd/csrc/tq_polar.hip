@@ -734,60 +734,77 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
   __syncthreads();
 }
 
-// q' = P q (or q), u = S q', and the tables of one head per workgroup.
+// q' = P q (or q), u = S q', and the tables of one head.  Grid (heads,
+// kP7PrepParts): the workgroups of a head each recompute q' and u (two
+// 128 x 128 products, two threads per output) and write their share of the
+// tables.  The rows of P and S are loaded before the first wait.
+constexpr int kP7PrepParts = 4;
 __global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, const float* P,
                                                              const float* S, const float* cs,
                                                              float* qtab, float* q_rot,
                                                              float* q_sketch) {
   __shared__ float xs[128], qp[128], u[128], csl[40];
-  const int h = blockIdx.x, t = threadIdx.x;
+  const int h = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
+  const int i = t >> 1, half = t & 1;  // output row, half of its dot product
+  const float4* srow = reinterpret_cast<const float4*>(S + i * 128 + 64 * half);
+  const float4* prow = reinterpret_cast<const float4*>((P ? P : S) + i * 128 + 64 * half);
+  float4 pr[16], sr[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    pr[c] = prow[c];
+    sr[c] = srow[c];
+  }
   if (t < 128) xs[t] = q[static_cast<int64_t>(h) * 128 + t];
   if (t < 40) csl[t] = cs[t];
   __syncthreads();
-  if (t < 128) {
-    float acc = xs[t];
-    if (P) {
-      acc = 0.0f;
-      const float* pr = P + t * 128;
-      for (int d = 0; d < 128; d += 4) {
-        const float4 a = *reinterpret_cast<const float4*>(pr + d);
-        acc = fmaf(xs[d], a.x, acc);
-        acc = fmaf(xs[d + 1], a.y, acc);
-        acc = fmaf(xs[d + 2], a.z, acc);
-        acc = fmaf(xs[d + 3], a.w, acc);
-      }
+  float acc = 0.0f;
+  if (P) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const float* x = xs + 64 * half + 4 * c;
+      acc = fmaf(x[0], pr[c].x, acc);
+      acc = fmaf(x[1], pr[c].y, acc);
+      acc = fmaf(x[2], pr[c].z, acc);
+      acc = fmaf(x[3], pr[c].w, acc);
     }
-    qp[t] = acc;
-    if (q_rot) q_rot[static_cast<int64_t>(h) * 128 + t] = acc;
+  } else {
+    acc = half == 0 ? xs[i] : 0.0f;
+  }
+  acc += shfl_xor_f(acc, 1);
+  if (half == 0) {
+    qp[i] = acc;
+    if (q_rot && part == 0) q_rot[static_cast<int64_t>(h) * 128 + i] = acc;
   }
   __syncthreads();
-  if (t < 128) {
-    const float* sr = S + t * 128;
-    float acc = 0.0f;
-    for (int d = 0; d < 128; d += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(sr + d);
-      acc = fmaf(qp[d], a.x, acc);
-      acc = fmaf(qp[d + 1], a.y, acc);
-      acc = fmaf(qp[d + 2], a.z, acc);
-      acc = fmaf(qp[d + 3], a.w, acc);
-    }
-    u[t] = acc;
-    if (q_sketch) q_sketch[static_cast<int64_t>(h) * 128 + t] = acc;
+  float us = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const float* x = qp + 64 * half + 4 * c;
+    us = fmaf(x[0], sr[c].x, us);
+    us = fmaf(x[1], sr[c].y, us);
+    us = fmaf(x[2], sr[c].z, us);
+    us = fmaf(x[3], sr[c].w, us);
+  }
+  us += shfl_xor_f(us, 1);
+  if (half == 0) {
+    u[i] = us;
+    if (q_sketch && part == 0) q_sketch[static_cast<int64_t>(h) * 128 + i] = us;
   }
   __syncthreads();
   float* out = qtab + static_cast<int64_t>(h) * kP7QTab;
-  for (int i = t; i < 1024; i += 256) {
-    const int j = i >> 4, c = i & 15;
-    out[i] = qp[2 * j] * csl[2 * c] + qp[2 * j + 1] * csl[2 * c + 1];
+  constexpr int kT1 = 1024 / kP7PrepParts, kTq = 4096 / kP7PrepParts;
+  for (int e = kT1 * part + t; e < kT1 * (part + 1); e += 256) {
+    const int j = e >> 4, c = e & 15;
+    out[e] = qp[2 * j] * csl[2 * c] + qp[2 * j + 1] * csl[2 * c + 1];
   }
-  for (int i = t; i < 4096; i += 256) {
-    const int pos = i >> 8, bits = i & 255;
+  for (int e = kTq * part + t; e < kTq * (part + 1); e += 256) {
+    const int pos = e >> 8, bits = e & 255;
     float sum = 0.0f;
 #pragma unroll
     for (int b = 0; b < 8; ++b) sum += ((bits >> b) & 1) ? u[8 * pos + b] : 0.0f;
-    out[1024 + i] = sum;
+    out[1024 + e] = sum;
   }
-  if (t < 64) {
+  if (part == 0 && t < 64) {
     const float sum = wave_sum_f(u[t] + u[t + 64]);
     if (t < 16) out[5120 + t] = t == 0 ? sum : 0.0f;
   }
@@ -1608,7 +1625,7 @@ int tq_polar7_prepare_query(const float* q, const float* precondition, const flo
   TQ_CHECK_ARG(num_heads >= 0 && num_heads <= 65535, "%s: bad num_heads", fn);
   TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(q_tables) % 16 == 0, "%s: q_tables must be 16-byte aligned", fn);
   if (num_heads == 0) return TQ_OK;
-  polar7_prepare_kernel<<<num_heads, 256, 0, static_cast<hipStream_t>(stream)>>>(
+  polar7_prepare_kernel<<<dim3(num_heads, kP7PrepParts), 256, 0, static_cast<hipStream_t>(stream)>>>(
       q, precondition, sketch, cs_tables, q_tables, q_rot, q_sketch);
   TQ_CHECK_LAUNCH("polar7_prepare_kernel");
   return TQ_OK;
