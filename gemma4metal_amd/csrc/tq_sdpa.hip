@@ -408,8 +408,11 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   // covers this: more groups never means more splits.)
   const char* impl = std::getenv("TQ_SDPA_IMPL");
   const bool try_mfma = !(impl && std::string(impl) == "valu");
+  // With GQA a multiple of 8, D = 512 runs the heads-as-columns kernel
+  // (8 heads per workgroup, each K/V byte unpacked once).
+  const bool hc = try_mfma && D == 512 && sb_dtype == TQ_F16 && gqa % 8 == 0;
   int G = head_subgroup(gqa);
-  if (try_mfma && D == 512 && sb_dtype == TQ_F16) G = gqa % 2 == 0 ? 2 : 1;
+  if (try_mfma && D == 512 && sb_dtype == TQ_F16 && !hc) G = gqa % 2 == 0 ? 2 : 1;
   const int n_sub = gqa / G;
   const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
   int eff_len = max_len;
@@ -449,6 +452,14 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
 
   dim3 grid(max_splits, Hkv * n_sub, batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (hc) {
+    // 8 heads x 512 dims of partials per split: merged by a separate,
+    // parallel kernel rather than one workgroup per kv head
+    p.ext_merge = max_splits > 1 ? 1 : 0;
+    const int r = launch_sdpa_hc(p, grid, s);
+    if (r != TQ_OK || !p.ext_merge) return r;
+    return launch_merge_splits(p, D, batch, s);
+  }
   if (try_mfma) {
     const int r = launch_sdpa_mfma(p, D, G, sb_dtype, grid, s);
     if (r >= 0) return r;

@@ -41,6 +41,9 @@ struct SdpaParams {
   // lib/turboquant.metal:886); > 0 -> out = O / (l + denom_eps)
   // (sdpa_tq_sequential, lib/turboquant.metal:222).
   float denom_eps;
+  // 0: the last workgroup of a split sequence merges the partials; 1: the
+  // kernel only writes them and launch_merge_splits merges them afterwards.
+  int ext_merge;
 };
 
 // The keys one workgroup attends: rows [t_begin, t_end) of its sequence's
@@ -164,7 +167,7 @@ struct Finalize {
         }
       }
     }
-    if (S == 1) return;
+    if (S == 1 || p.ext_merge) return;
 
     // The last workgroup of this (sequence, kv head, subgroup) to finish merges
     // the splits.  Partials are written with agent-scope stores (write-through
@@ -240,5 +243,11 @@ WsLayout ws_layout(int batch, int Hq, int D, int max_splits);
 // a tq_status error, or -1 when (D, G) is not served by that kernel.
 int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
                      hipStream_t stream);
+// D = 512, 8 query heads per workgroup (heads as matrix-core columns), fp16
+// scale/bias: tq_sdpa_hc.hip.
+int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t stream);
+// Merge of the split partials of a launch with ext_merge = 1 (batch b of
+// grid.y): tq_sdpa_hc.hip.
+int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t stream);
 
 }  // namespace tq

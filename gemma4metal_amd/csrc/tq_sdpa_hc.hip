@@ -1,0 +1,481 @@
+// Decode attention at head_dim 512 with eight query heads per kv head (Gemma
+// global layers, GQA 8: engine/gemma4_multilayer.cpp:3,49-51), on the matrix
+// cores with the query heads as MFMA columns.
+//
+// Same contract, split and finalisation as the kernels of tq_sdpa.hip and
+// tq_sdpa_mfma.hip (replaces sdpa_int4_vector<512>, lib/turboquant.metal:
+// 723-889, 898-903).  That kernel fills its 16 columns with (head, quant
+// group) pairs, which at D = 512 leaves room for 2 heads, so a kv head needs
+// 4 workgroups that each unpack the same K/V.  Here one workgroup takes all
+// 8 heads of a kv head, so every K/V byte is unpacked once:
+//
+// K . q  -- per quant group g (64 dims): v_mfma_i32_16x16x64_i8 with A = 16
+//   keys x 64 nibbles of group g and B = q of the 8 heads (columns 0-7,
+//   repeated in 8-15) as three signed base-256 digits of round(q * 2^F), so
+//   C[key][head] is the exact integer dot of group g.  The score is
+//   sum_g s_g * 2^-F * dot_g + b_g * sum(q over g), taken in every lane of
+//   column (head) and (head + 8).
+// P . V  -- v_mfma_f32_16x16x32_bf16 per block of 16 V words (2 quant
+//   groups): A = (128 + nibble) as bf16 of 16 words x 32 keys (v_perm_b32 +
+//   and-or), B = the bf16 hi / lo split of p * s_v in columns (head, group of
+//   the block), column head + 8 g' taking the block's second group.  bf16
+//   keeps fp32's exponent range, so no V scale overflows the weights.  The
+//   128 offset (128 * sum of the weights) and the bias term sum(p * b_v) are
+//   kept per (column, block) and removed at the end.
+//
+// Lane roles (l = lane, m = l % 16, c = l / 16):
+//   K A-operand: key 16 tile + m, words 8 g + 2c, 8 g + 2c + 1 of group g;
+//   scores: C rows 4c .. 4c+3 of column m, i.e. keys 16 tile + 4c + i of
+//   head m % 8;  V slot j of lane group c: key 16 (j / 4) + 4c + j % 4 (the
+//   key whose weight this lane computed as C[4c + j % 4] of tile j / 4);
+//   V A-operand row m of block blk: word 16 blk + m.
+// Four waves, one per SIMD (the P.V accumulators of 8 heads x 512 dims take
+// 128 registers); loads double-buffered one 32-key iteration ahead.
+#include "tq_sdpa_common.h"
+
+namespace tq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int kHcWaves = 4;
+constexpr int kHcD = 512;
+constexpr int kHcG = 8;    // query heads per workgroup
+constexpr int kHcNG = 8;   // quant groups per row
+constexpr int kHcRB = 256; // bytes per packed row
+
+struct HcBuf {
+  uint32_t kw[2][16];  // [tile][2 g + e]: word 8 g + 2c + e of key 16 tile + m
+  uint32_t vw[8][4];   // [slot][blk]: word 16 blk + m of the slot's key
+  uint32_t sc[2][4];   // scales of array c for keys 2m, 2m+1 (8 fp16 each)
+};
+
+// Loads of the 32 keys at t0 (rows clamped to `last`, the uniform limit
+// `lim` = last - t0 >= 0), non-temporal, uniform base + 32-bit lane offset.
+__device__ __forceinline__ void hc_load(HcBuf& B, const char* kq, const char* vq, const char* sc,
+                                        int t0, int lim, int m, int c) {
+  const char* kb = kq + static_cast<int64_t>(t0) * kHcRB;
+  const char* vb = vq + static_cast<int64_t>(t0) * kHcRB;
+  const char* sb = sc + static_cast<int64_t>(t0) * 16;
+#pragma unroll
+  for (int tile = 0; tile < 2; ++tile) {
+    const uint32_t off = static_cast<uint32_t>(min(16 * tile + m, lim)) * kHcRB + c * 8;
+#pragma unroll
+    for (int g = 0; g < kHcNG; ++g) {
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(kb + off + 32 * g));
+      B.kw[tile][2 * g] = u.x;
+      B.kw[tile][2 * g + 1] = u.y;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t off = static_cast<uint32_t>(min(16 * (j >> 2) + 4 * c + (j & 3), lim)) * kHcRB + m * 4;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+      B.vw[j][blk] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb + off + 64 * blk));
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint32_t off = static_cast<uint32_t>(min(2 * m + e, lim)) * 16;
+    const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sb + off));
+    B.sc[e][0] = u.x; B.sc[e][1] = u.y; B.sc[e][2] = u.z; B.sc[e][3] = u.w;
+  }
+}
+
+__device__ __forceinline__ float hc_half(uint32_t w, int hi) {
+  return __half2float(__ushort_as_half(static_cast<uint16_t>(hi ? (w >> 16) : (w & 0xFFFFu))));
+}
+
+__global__ __launch_bounds__(kHcWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void sdpa_int4_hc_kernel(SdpaParams p) {
+  constexpr int NW = kHcWaves, D = kHcD, G = kHcG, NG = kHcNG;
+  constexpr int kNT = NW * 64;
+  constexpr int kIter = 32 * NW;          // keys per workgroup iteration
+  constexpr int NE = G * D / kNT;         // q elements per thread
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, c = lane >> 4;
+  const int hh = m & 7;                   // this lane's head (column m)
+  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+
+  const SplitRange rg = split_range(p, b, split);
+  if (split >= rg.S) return;
+  const int t_end = rg.t_end;
+
+  using Fin = Finalize<G, D, NW>;
+  __shared__ float arena[Fin::kArena];
+  __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][group][lane]
+  __shared__ uint32_t sc_lds[NW][4][NG][16];    // [wave][array][group][key pair] fp16 x 2
+  __shared__ float red_max[NE][NW];
+  __shared__ float sh_qhat[G][NG];
+  __shared__ int sh_F[G];
+
+  const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
+  const char* kq_rows = reinterpret_cast<const char*>(p.kq + row0 * (D / 8));
+  const char* vq_rows = reinterpret_cast<const char*>(p.vq + row0 * (D / 8));
+  // lane group c loads scale array c: k scale, k bias, v scale, v bias
+  const void* sc_base = c == 0 ? p.ks : (c == 1 ? p.kb : (c == 2 ? p.vs : p.vb));
+  const char* sc_rows = static_cast<const char*>(sc_base) + row0 * 16;
+
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int base0 = rg.t_begin + wv * 32;
+  const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
+  const int last = t_end - 1;
+  const int safe_last = max(last, 0);
+
+  // q first (one dword per element, no branch around the load), then the
+  // first iteration's K/V, which stay in flight through the prologue
+  uint32_t qraw[NE];
+  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
+    qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
+    if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  HcBuf bufA, bufB;
+  {
+    const int t0 = min(base0, safe_last);
+    hc_load(bufA, kq_rows, vq_rows, sc_rows, t0, safe_last - t0, m, c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- prologue: q of the 8 heads as 22-bit fixed point, B images in LDS --
+  float qv[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const uint32_t w = qraw[k];
+    const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
+                    : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
+                                          : __uint_as_float(w << 16);
+    qv[k] = f * p.scale_log2;
+  }
+  // slot (k, w) = elements 64 w + kNT k + lane: one quant group of head
+  // (kNT k) / D (kNT divides D, so k alone names the head)
+  static_assert(D % kNT == 0, "slot -> head");
+  constexpr int KPH = D / kNT;  // slots k per head
+  // the NE wave reductions step through the shuffle offsets together, so
+  // their LDS round trips overlap
+  {
+    float mx[NE];
+#pragma unroll
+    for (int k = 0; k < NE; ++k) mx[k] = fabsf(qv[k]);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1)
+#pragma unroll
+      for (int k = 0; k < NE; ++k) mx[k] = fmaxf(mx[k], shfl_xor_f(mx[k], off));
+    if (lane == 0) {
+#pragma unroll
+      for (int k = 0; k < NE; ++k) red_max[k][wave] = mx[k];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const int h = threadIdx.x;
+    float hm = 0.0f;
+#pragma unroll
+    for (int k2 = 0; k2 < KPH; ++k2)
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2) hm = fmaxf(hm, red_max[h * KPH + k2][w2]);
+    int ex = 0;
+    if (hm > 0.0f) frexpf(hm, &ex);  // hm < 2^ex
+    sh_F[h] = 22 - ex;               // |round(q * 2^F)| <= 2^22
+  }
+  __syncthreads();
+  uint8_t* bq_bytes = reinterpret_cast<uint8_t*>(&bq_lds[0][0][0]);
+  int X[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int h = k / KPH;
+    const int d = (wave * 64 + k * kNT - h * D) + lane;
+    X[k] = static_cast<int>(__builtin_rintf(qv[k] * ldexpf(1.0f, sh_F[h])));
+    // k-slot of dim d in the A operand of group g = d / 64: lane group
+    // cc = (d % 64) / 16, vector element v = 2 ((d % 16) / 8) + d % 2, byte
+    // (d % 8) / 2 -- the order in which the unpack spreads a word's nibbles
+    const int g = d >> 6, r = d & 63, cc = r >> 4, rr = r & 15;
+    const int s = 4 * (2 * (rr >> 3) + (rr & 1)) + ((rr & 7) >> 1);
+    const int d0 = static_cast<int8_t>(X[k] & 0xFF);
+    const int X1 = (X[k] - d0) >> 8;
+    const int d1 = static_cast<int8_t>(X1 & 0xFF);
+    const int d2 = (X1 - d1) >> 8;
+#pragma unroll
+    for (int dup = 0; dup < 2; ++dup) {
+      const int ln = 16 * cc + h + 8 * dup;
+      const int o = ((g * 64) + ln) * 16 + s;
+      bq_bytes[o] = static_cast<uint8_t>(d0);
+      bq_bytes[o + NG * 64 * 16] = static_cast<uint8_t>(d1);
+      bq_bytes[o + 2 * NG * 64 * 16] = static_cast<uint8_t>(d2);
+    }
+  }
+  // per (head, quant group) sums of the fixed-point q, exact: 64 * 2^22 < 2^31
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1)
+#pragma unroll
+    for (int k = 0; k < NE; ++k) X[k] += __shfl_xor(X[k], off, 64);
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      const int h = k / KPH, g = (wave * 64 + k * kNT - h * D) >> 6;
+      sh_qhat[h][g] = static_cast<float>(X[k]) * ldexpf(1.0f, -sh_F[h]);
+    }
+  }
+  __syncthreads();
+  const float sf = ldexpf(1.0f, -sh_F[hh]);
+  float qh[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) qh[g] = sh_qhat[hh][g];
+
+  // ---- main loop ----------------------------------------------------------
+  float m_run = -INFINITY, l_run = 0.0f;
+  float wsum[4], bacc[4];  // per V block: sum of the weights, sum of p * b_v
+  v4f cv[4][8];            // [blk][2 byte + nibble half]
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    wsum[blk] = 0.0f;
+    bacc[blk] = 0.0f;
+#pragma unroll
+    for (int f = 0; f < 8; ++f) cv[blk][f] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  uint32_t magic = 0x43004300u;  // bf16 of (128 + nibble)
+  asm volatile("" : "+v"(magic));
+  const v4i zero4 = v4i{0, 0, 0, 0};
+
+  auto process = [&](const HcBuf& B, int t0) {
+    // scales -> LDS [array][group][key pair]
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const uint32_t a0 = B.sc[0][g >> 1], a1 = B.sc[1][g >> 1];
+      sc_lds[wv][c][g][m] = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u)) : ((a0 & 0xFFFFu) | (a1 << 16));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // K . q per quant group, both 16-key tiles
+    float sc[2][4];
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[tile][i] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const uint4 u0 = bq_lds[0][g][lane], u1 = bq_lds[1][g][lane], u2 = bq_lds[2][g][lane];
+      const v4i b0 = v4i{static_cast<int>(u0.x), static_cast<int>(u0.y), static_cast<int>(u0.z), static_cast<int>(u0.w)};
+      const v4i b1 = v4i{static_cast<int>(u1.x), static_cast<int>(u1.y), static_cast<int>(u1.z), static_cast<int>(u1.w)};
+      const v4i b2 = v4i{static_cast<int>(u2.x), static_cast<int>(u2.y), static_cast<int>(u2.z), static_cast<int>(u2.w)};
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        const uint32_t w0 = B.kw[tile][2 * g], w1 = B.kw[tile][2 * g + 1];
+        const v4i a = v4i{static_cast<int>(w0 & 0x0F0F0F0Fu), static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
+                          static_cast<int>(w1 & 0x0F0F0F0Fu), static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+        const v4i acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b0, zero4, 0, 0, 0);
+        const v4i acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b1, zero4, 0, 0, 0);
+        const v4i acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b2, zero4, 0, 0, 0);
+        const uint2 ks = *reinterpret_cast<const uint2*>(&sc_lds[wv][0][g][8 * tile + 2 * c]);
+        const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[wv][1][g][8 * tile + 2 * c]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
+          const int lo01 = acc0[i] + (acc1[i] << 8);
+          const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc2[i]);
+          const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
+          sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[g], sc[tile][i]));
+        }
+      }
+    }
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (t0 + 16 * tile + 4 * c + i >= t_end) sc[tile][i] = -INFINITY;
+
+    // online softmax over the 32 keys, per head (column)
+    float mt = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    if (__any(m_new > m_run)) {
+      const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
+      l_run *= f;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        wsum[blk] *= f;
+        bacc[blk] *= f;
+#pragma unroll
+        for (int ff = 0; ff < 8; ++ff) cv[blk][ff] *= f;
+      }
+      m_run = m_new;
+    }
+    float pw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sj = sc[j >> 2][j & 3];
+      pw[j] = sj == -INFINITY ? 0.0f : fast_exp2(sj - m_run);
+      l_run += pw[j];
+    }
+
+    // P . V per block of 16 V words (quant groups 2 blk, 2 blk + 1)
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int gv = 2 * blk + (m >> 3);
+      const uint2 vs0 = *reinterpret_cast<const uint2*>(&sc_lds[wv][2][gv][2 * c]);
+      const uint2 vs1 = *reinterpret_cast<const uint2*>(&sc_lds[wv][2][gv][8 + 2 * c]);
+      const uint2 vb0 = *reinterpret_cast<const uint2*>(&sc_lds[wv][3][gv][2 * c]);
+      const uint2 vb1 = *reinterpret_cast<const uint2*>(&sc_lds[wv][3][gv][8 + 2 * c]);
+      const uint32_t vsw[4] = {vs0.x, vs0.y, vs1.x, vs1.y};
+      const uint32_t vbw[4] = {vb0.x, vb0.y, vb1.x, vb1.y};
+      __bf16 hi[8], lo[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float w = pw[j] * hc_half(vsw[j >> 1], j & 1);
+        hi[j] = static_cast<__bf16>(w);
+        const float hf = static_cast<float>(hi[j]);
+        lo[j] = static_cast<__bf16>(w - hf);
+        wsum[blk] += hf + static_cast<float>(lo[j]);
+        bacc[blk] = fmaf(pw[j], hc_half(vbw[j >> 1], j & 1), bacc[blk]);
+      }
+      const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+      const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+#pragma unroll
+      for (int by = 0; by < 4; ++by) {
+        const uint32_t sel = static_cast<uint32_t>(by) | (0x0Cu << 8) |
+                             (static_cast<uint32_t>(4 + by) << 16) | (0x0Cu << 24);
+        uint32_t alo[4], ahi[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t x = __builtin_amdgcn_perm(B.vw[2 * r + 1][blk], B.vw[2 * r][blk], sel);
+          alo[r] = (x & 0x000F000Fu) | magic;
+          ahi[r] = ((x >> 4) & 0x000F000Fu) | magic;
+        }
+        const v8bf a_lo = __builtin_bit_cast(v8bf, u32x4{alo[0], alo[1], alo[2], alo[3]});
+        const v8bf a_hi = __builtin_bit_cast(v8bf, u32x4{ahi[0], ahi[1], ahi[2], ahi[3]});
+        cv[blk][2 * by] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, bhi, cv[blk][2 * by], 0, 0, 0);
+        cv[blk][2 * by + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, bhi, cv[blk][2 * by + 1], 0, 0, 0);
+        cv[blk][2 * by] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, blo, cv[blk][2 * by], 0, 0, 0);
+        cv[blk][2 * by + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, blo, cv[blk][2 * by + 1], 0, 0, 0);
+      }
+    }
+  };
+
+  auto load_next = [&](HcBuf& B, int t0) {
+    const int tc = min(t0, last);
+    hc_load(B, kq_rows, vq_rows, sc_rows, tc, last - tc, m, c);
+  };
+
+  for (int it = 0; it < nit; it += 2) {
+    load_next(bufB, base0 + (it + 1) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    process(bufA, base0 + it * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    load_next(bufA, base0 + (it + 2) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < nit) process(bufB, base0 + (it + 1) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // ---- per-wave result into the finalisation arena --------------------------
+  // lane (m, c) holds V words 16 blk + 4c + i of column m; the column's
+  // group in block blk is 2 blk + m / 8, the words' group 2 blk + c / 2
+  float l_sum = l_run + shfl_xor_f(l_run, 16);
+  l_sum += shfl_xor_f(l_sum, 32);
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    wsum[blk] += shfl_xor_f(wsum[blk], 16);
+    wsum[blk] += shfl_xor_f(wsum[blk], 32);
+    bacc[blk] += shfl_xor_f(bacc[blk], 16);
+    bacc[blk] += shfl_xor_f(bacc[blk], 32);
+  }
+  if ((c >> 1) == (m >> 3)) {
+    float* o = Fin::o(arena, wave, hh);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const float off = bacc[blk] - 128.0f * wsum[blk];
+#pragma unroll
+      for (int f = 0; f < 8; ++f)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[8 * (16 * blk + 4 * c + i) + f] = cv[blk][f][i] + off;
+    }
+  }
+  if (c == 0 && m < 8) {
+    Fin::m(arena, wave)[hh] = m_run;
+    Fin::l(arena, wave)[hh] = l_sum;
+  }
+  Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
+}
+
+// Merge of split partials written with ext_merge = 1: eight outputs (four
+// dims each) per wave, eight lanes per output taking every eighth split,
+// combined with three shuffles.  The partials come from an earlier kernel,
+// so plain loads see them.  Grid (ceil(Hq * D / 4 / 32), batch).
+__global__ __launch_bounds__(256) void merge_splits_kernel(SdpaParams p, int D) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sl = lane & 7;
+  const int D4 = D / 4;
+  const int o0 = (blockIdx.x * 4 + wave) * 8;  // first output of this wave
+  const int b = blockIdx.y;
+  if (o0 >= p.Hq * D4) return;                 // whole waves (Hq * D4 % 8 == 0)
+  const SplitRange rg = split_range(p, b, 0);
+  const int S = rg.S;
+  if (S == 1) return;                          // written by the attention kernel
+  const int o = o0 + (lane >> 3);
+  const int h = o / D4, d4 = o - h * D4;
+  const int64_t head = static_cast<int64_t>(b) * p.Hq + h;
+  const float* ml = p.ws_ml + head * p.max_splits * 2;
+  float M = -INFINITY;
+  for (int s = sl; s < S; s += 8) M = fmaxf(M, ml[2 * s]);
+  M = fmaxf(M, shfl_xor_f(M, 1));
+  M = fmaxf(M, shfl_xor_f(M, 2));
+  M = fmaxf(M, shfl_xor_f(M, 4));
+  float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float L = 0.0f;
+  for (int s = sl; s < S; s += 8) {
+    const float f = merge_factor(ml[2 * s], M);
+    const float4 v = *reinterpret_cast<const float4*>(p.ws_o + (head * p.max_splits + s) * D + 4 * d4);
+    O.x = fmaf(v.x, f, O.x);
+    O.y = fmaf(v.y, f, O.y);
+    O.z = fmaf(v.z, f, O.z);
+    O.w = fmaf(v.w, f, O.w);
+    L = fmaf(ml[2 * s + 1], f, L);
+  }
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) {
+    O.x += shfl_xor_f(O.x, off);
+    O.y += shfl_xor_f(O.y, off);
+    O.z += shfl_xor_f(O.z, off);
+    O.w += shfl_xor_f(O.w, off);
+    L += shfl_xor_f(L, off);
+  }
+  if (sl == 0) {
+    float* out = p.out + head * D + 4 * d4;
+    out[0] = normalise(O.x, L, p.denom_eps);
+    out[1] = normalise(O.y, L, p.denom_eps);
+    out[2] = normalise(O.z, L, p.denom_eps);
+    out[3] = normalise(O.w, L, p.denom_eps);
+  }
+}
+
+}  // namespace
+
+int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t s) {
+  const int outs = p.Hq * D / 4;
+  merge_splits_kernel<<<dim3((outs + 31) / 32, batch), 256, 0, s>>>(p, D);
+  TQ_CHECK_LAUNCH("merge_splits_kernel");
+  return TQ_OK;
+}
+
+int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t s) {
+  sdpa_int4_hc_kernel<<<grid, kHcWaves * 64, 0, s>>>(p);
+  TQ_CHECK_LAUNCH("sdpa_int4_hc_kernel");
+  return TQ_OK;
+}
+
+}  // namespace tq

@@ -12,15 +12,16 @@
 //   group's dims, so C[key][(h,g)] is the exact integer partial dot of group g.
 //   The fp32 score is sum_g s_g * 2^-F * dot_g + b_g * sum(q over g), the
 //   (h,g) columns being folded with a DPP butterfly.
-// P . V  -- v_mfma_f32_16x16x32_f16.  A = 16 dims x 32 keys, built by
+// P . V  -- v_mfma_f32_16x16x32_bf16.  A = 16 dims x 32 keys, built by
 //   v_perm_b32 gathering one byte of two keys' words and an and-or with the
-//   fp16 magic 0x6400 (1024 + nibble); B = the softmax weights p*s_v*1024
-//   split into fp16 hi + lo parts (22-bit), again in (h,g) columns.  The 1024
+//   bf16 magic 0x4300 (128 + nibble); B = the softmax weights p*s_v split
+//   into bf16 hi + lo parts (~16 bits), again in (h,g) columns.  bf16 keeps
+//   fp32's exponent range, so no V scale can overflow the weights.  The 128
 //   offset is removed at the end from the running sum of the weights.
 //
 // Lane roles (l = lane, m = l % 16, c = l / 16; layouts checked on hardware):
 //   A rows / B cols / C cols = m;  k-slot j of lane-group c is k = 8c + j
-//   (f16) or 16c + 4v + byte (i8);  C rows held by lane-group c: 4c .. 4c+3.
+//   (bf16) or 16c + 4v + byte (i8);  C rows held by lane-group c: 4c .. 4c+3.
 //   Key of V slot j in lane-group c: t0 + 16*(j/4) + 4c + (j%4), which is the
 //   K tile (j/4), C row 4c + (j%4): the softmax weights are produced by the
 //   K MFMAs exactly in the lanes and slots the V MFMAs consume them from.
@@ -40,7 +41,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 template <int D, int G>
 struct MGeom {
@@ -54,7 +55,7 @@ struct MGeom {
   // and the accumulators then fit two waves per SIMD)
   static constexpr int VS = D == 512 ? 2 : 1;
   static constexpr int VWH = VW / VS;   // V words per lane per key of one wave
-  static constexpr int VM = 8 * VWH;    // f16 accumulator tiles of one wave
+  static constexpr int VM = 8 * VWH;    // P.V accumulator tiles of one wave
   static constexpr int SCW = NG / 2;    // 32-bit words of one key's scales
   static_assert(COLS <= 16, "more than 16 (head, group) columns");
   static_assert(D == 128 || D == 256 || D == 512, "D");
@@ -306,9 +307,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   v4f cv[VM];
 #pragma unroll
   for (int f = 0; f < VM; ++f) cv[f] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  // fp16 magic of (1024 + nibble), kept in a VGPR so each A-operand word is
+  // bf16 magic of (128 + nibble), kept in a VGPR so each A-operand word is
   // one v_and_or_b32 (a gfx9 VOP3 instruction takes at most one literal/SGPR)
-  uint32_t magic = 0x64006400u;
+  uint32_t magic = 0x43004300u;
   asm volatile("" : "+v"(magic));
 
   auto process = [&](const IterBuf<D>& B, int t0) {
@@ -372,9 +373,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       }
     }
 
-    // online softmax over the 32 keys (log2 domain); the weights are kept
-    // scaled by 2^10 (p' = exp2(s - m + 10)) so their fp16 hi/lo split stays
-    // in the normal range -- the same factor is in l, so it cancels.
+    // online softmax over the 32 keys (log2 domain)
     float mt = sc[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
@@ -390,29 +389,26 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       for (int ff = 0; ff < VM; ++ff) cv[ff] *= f;
       m_run = m_new;
     }
-    const float m10 = m_run - 10.0f;
-    _Float16 hi[8], lo[8];
+    __bf16 hi[8], lo[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int tile = j >> 2, i = j & 3;
-      const float pj = sc[j] == -INFINITY ? 0.0f : fast_exp2(sc[j] - m10);
+      const float pj = sc[j] == -INFINITY ? 0.0f : fast_exp2(sc[j] - m_run);
       l_run += pj;
       const uint32_t vspair = scv[2][tile][i >> 1], vbpair = scv[3][tile][i >> 1];
       const float vs = (i & 1) ? half_hi(vspair) : half_lo(vspair);
       const float vb = (i & 1) ? half_hi(vbpair) : half_lo(vbpair);
       bacc = fmaf(pj, vb, bacc);
       const float w = pj * vs;
-      hi[j] = static_cast<_Float16>(w);
-      lo[j] = static_cast<_Float16>(w - static_cast<float>(hi[j]));
-      wsum += w;
+      hi[j] = static_cast<__bf16>(w);
+      const float hf = static_cast<float>(hi[j]);
+      lo[j] = static_cast<__bf16>(w - hf);
+      wsum += hf + static_cast<float>(lo[j]);
     }
-    const v8h bhi = v8h{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
-    const v8h blo = v8h{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
-    const v8h sixteenth = v8h{0.0625f16, 0.0625f16, 0.0625f16, 0.0625f16,
-                              0.0625f16, 0.0625f16, 0.0625f16, 0.0625f16};
-    const v8h bhi16 = bhi * sixteenth, blo16 = blo * sixteenth;
+    const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+    const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
 
-    // P . V on the f16 matrix cores: A = (1024 + nibble) of 16 dims x 32 keys
+    // P . V on the bf16 matrix cores: A = (128 + nibble) of 16 dims x 32 keys
 #pragma unroll
     for (int s = 0; s < VWH; ++s) {
 #pragma unroll
@@ -424,19 +420,19 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         for (int r = 0; r < 4; ++r) {
           const uint32_t x = __builtin_amdgcn_perm(B.vw[2 * r + 1][s], B.vw[2 * r][s], sel);
           alo[r] = (x & 0x000F000Fu) | magic;
-          ahi[r] = (x & 0x00F000F0u) | magic;
+          ahi[r] = ((x >> 4) & 0x000F000Fu) | magic;
         }
         const v4i ilo = v4i{static_cast<int>(alo[0]), static_cast<int>(alo[1]),
                             static_cast<int>(alo[2]), static_cast<int>(alo[3])};
         const v4i ihi = v4i{static_cast<int>(ahi[0]), static_cast<int>(ahi[1]),
                             static_cast<int>(ahi[2]), static_cast<int>(ahi[3])};
-        const v8h a_lo = __builtin_bit_cast(v8h, ilo);
-        const v8h a_hi = __builtin_bit_cast(v8h, ihi);
+        const v8bf a_lo = __builtin_bit_cast(v8bf, ilo);
+        const v8bf a_hi = __builtin_bit_cast(v8bf, ihi);
         const int fe = 8 * s + 2 * by, fo = fe + 1;
-        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, bhi, cv[fe], 0, 0, 0);
-        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, bhi16, cv[fo], 0, 0, 0);
-        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, blo, cv[fe], 0, 0, 0);
-        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, blo16, cv[fo], 0, 0, 0);
+        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, bhi, cv[fe], 0, 0, 0);
+        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, bhi, cv[fo], 0, 0, 0);
+        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, blo, cv[fe], 0, 0, 0);
+        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, blo, cv[fo], 0, 0, 0);
       }
     }
   };
@@ -458,7 +454,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
   // ---- per-wave result into the finalisation arena --------------------------
   // The V MFMAs contract over the keys of all four lane groups, so the
-  // per-lane sums (softmax denominator, weight sum of the 1024 offset, bias
+  // per-lane sums (softmax denominator, weight sum of the 128 offset, bias
   // term) are totalled over the lane groups of the same column.
   float l_sum = l_run + shfl_xor_f(l_run, 16);
   l_sum += shfl_xor_f(l_sum, 32);
@@ -483,8 +479,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 #pragma unroll
             for (int so = 0; so < VWH; ++so)
               if (so == s) {
-                const float off = (j & 1) ? 64.0f : 1024.0f;
-                v = (cv[8 * so + j][i] - off * wsum) + bacc;
+                v = (cv[8 * so + j][i] - 128.0f * wsum) + bacc;
               }
             Fin::o(arena, wave, hn)[dim] = v;
           }

@@ -148,3 +148,79 @@ def test_workspace_reuse_across_shapes(gpu):
             qd, cd, ld, wd, ref = cases[i]
             out = gpu.sdpa_int4_ragged(qd, *cd, ld, 2, windows=wd)
             assert_close(host(out), ref, f"rep {rep} case {i}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,W,qdt", [
+    (32, 4, 5000, 0, "bf16"),     # Gemma global layer: many splits, partial last iteration
+    (32, 4, 3001, 1024, "bf16"),  # window active
+    (32, 2, 2100, 0, "f16"),      # GQA 16: two 8-head subgroups per kv head
+    (8, 1, 1, 0, "f32"),          # single key
+    (16, 2, 129, 0, "bf16"),
+])
+def test_sdpa_d512_gqa8(gpu, Hq, Hkv, L, W, qdt):
+    """D=512 with 8 query heads per kv head (the heads-as-columns kernel)."""
+    rng = np.random.default_rng(Hq * 131 + L * 7 + W)
+    qd, qv = queries(rng, (Hq, 512), qdt)
+    c = host_cache(rng, Hkv, L, 512, "f16")
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv, 1.0, W)
+    ref = O.sdpa_int4(qv, *c, Hq // Hkv, 1.0, W)
+    assert_close(host(out), ref, f"D512 Hq{Hq} Hkv{Hkv} L{L} W{W}")
+
+
+def test_sdpa_d512_gqa8_ragged(gpu):
+    rng = np.random.default_rng(51)
+    B, Hq, Hkv, D, cap = 3, 32, 4, 512, 1500
+    lens = np.array([1500, 1, 700], np.int32)
+    wins = np.array([0, 1024, 100], np.int32)
+    qd, qv = queries(rng, (B, Hq, D), "bf16")
+    k = O.rms_norm(rng.standard_normal((B, Hkv, cap, D)).astype(np.float32))
+    v = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    c = O.quantize_int4(k, "f16") + O.quantize_int4(v, "f16")
+    out = gpu.sdpa_int4_ragged(qd, *[dev(a) for a in c], dev(lens), 8, windows=dev(wins))
+    ref = O.sdpa_int4_ragged(qv, *c, lens, wins, 8)
+    assert_close(host(out), ref, "D512 ragged")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 16, 256), (32, 4, 512), (8, 2, 128), (8, 4, 512)])
+def test_sdpa_large_value_range(gpu, Hq, Hkv, D):
+    """V of magnitude ~1e3 (fp16 scales ~1e2): the matrix-core P.V weights
+    p * s_v must not overflow.  Tolerance scaled by the value magnitude."""
+    rng = np.random.default_rng(D + Hq)
+    mag = 300.0
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    k = O.rms_norm(rng.standard_normal((Hkv, 700, D)).astype(np.float32))
+    v = (rng.standard_normal((Hkv, 700, D)) * mag).astype(np.float32)
+    c = O.quantize_int4(k, "f16") + O.quantize_int4(v, "f16")
+    got = np.asarray(host(gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv)), np.float64)
+    ref = np.asarray(O.sdpa_int4(qv, *c, Hq // Hkv), np.float64)
+    assert np.all(np.isfinite(got)), "non-finite output"
+    d = np.abs(got - ref)
+    assert d.max() <= 2e-3 * mag, d.max()
+    assert np.linalg.norm(d) / np.linalg.norm(ref) <= 1e-3
+
+
+def test_sdpa_global_layer_full_context(gpu):
+    """Gemma global layer at 32k (Hq 32, Hkv 4, D 512): cache built on the GPU
+    by the (separately bit-exact) quantize kernel, two kv heads checked
+    against the C oracle."""
+    from oracle import coracle
+    Hq, Hkv, D, L = 32, 4, 512, 32768
+    g = torch.Generator(device="cuda").manual_seed(512)
+    kq = torch.empty((Hkv, L, D // 8), dtype=torch.uint32, device="cuda")
+    vq = torch.empty_like(kq)
+    ks = torch.empty((Hkv, L, D // 64), dtype=torch.float16, device="cuda")
+    kb, vs, vb = torch.empty_like(ks), torch.empty_like(ks), torch.empty_like(ks)
+    for h in range(Hkv):
+        k = torch.randn((L, D), generator=g, device="cuda")
+        k = k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)
+        v = torch.randn((L, D), generator=g, device="cuda")
+        kq[h], ks[h], kb[h] = gpu.quantize(k, scale_dtype=torch.float16)
+        vq[h], vs[h], vb[h] = gpu.quantize(v, scale_dtype=torch.float16)
+    rng = np.random.default_rng(78)
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    out = host(gpu.sdpa_int4(qd, kq, ks, kb, vq, vs, vb, 8))
+    for kvh in (0, 3):
+        sl = slice(kvh, kvh + 1)
+        c = [host(t[sl]) for t in (kq, ks, kb, vq, vs, vb)]
+        ref = coracle.sdpa_int4_f64(qv[8 * kvh:8 * kvh + 8], *c, 8)
+        assert_close(out[8 * kvh:8 * kvh + 8], ref, f"global L=32768 kv head {kvh}")
