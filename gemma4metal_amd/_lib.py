@@ -43,6 +43,7 @@ SIGNATURES = {
                                 P, SZ, P]),
     "tq_quantize_int4": (I, [P, I, I64, I, I, I, I, P, P, P, I, P]),
     "tq_kv_append_int4": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, P, I, I, P]),
+    "tq_kv_append_int4_ring": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, P, I, I, P]),
     "tq_dequantize_int4": (I, [P, P, P, I, I64, I, P, P]),
     "tq_polar_quantize": (I, [P, P, P, P, I64, I, I, P, P, P, P, P, P]),
     "tq_polar_quantize_packed": (I, [P, P, P, P, I64, I, I, P, P, P, P, P, P]),

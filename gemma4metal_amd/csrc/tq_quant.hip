@@ -29,6 +29,7 @@ struct QuantParams {
   int heads;            // append: kv heads per sequence
   int n_new;            // append: rows per (sequence, head)
   int cap;              // append: cache capacity (row stride per head)
+  int ring;             // append: rows (pos[b] + t) mod cap, last cap rows of n_new only
 };
 
 __device__ __forceinline__ void load8(const void* x, int dtype, int64_t off, float v[8]) {
@@ -110,7 +111,13 @@ __global__ __launch_bounds__(256) void quantize_int4_kernel(QuantParams p) {
     const int64_t bh = row / p.n_new;
     const int t = static_cast<int>(row - bh * p.n_new);
     const int64_t b = bh / p.heads;
-    const int dst = p.pos[b] + t;
+    int dst = p.pos[b] + t;
+    if (p.ring) {
+      // a ring keeps the newest cap rows: older rows of this append would
+      // land on the same slots, so they are not written at all
+      if (p.pos[b] < 0 || t < p.n_new - p.cap) return;
+      dst %= p.cap;
+    }
     if (dst < 0 || dst >= p.cap) return;
     drow = bh * p.cap + dst;
   }
@@ -204,25 +211,25 @@ extern "C" int tq_quantize_int4(const void* x, tq_dtype x_dtype, int64_t rows, i
   return launch_quantize(p, 1, sb_dtype, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int tq_kv_append_int4(const void* k_new, const void* v_new, tq_dtype x_dtype,
-                                 uint32_t* k_quant, void* k_scales, void* k_biases,
-                                 uint32_t* v_quant, void* v_scales, void* v_biases,
-                                 tq_dtype sb_dtype, int batch, int num_kv_heads, int head_dim,
-                                 int kv_capacity, const int32_t* positions, int n_new,
-                                 tq_quant_mode mode, void* stream) {
+namespace {
+int kv_append(const void* k_new, const void* v_new, tq_dtype x_dtype, uint32_t* k_quant,
+              void* k_scales, void* k_biases, uint32_t* v_quant, void* v_scales, void* v_biases,
+              tq_dtype sb_dtype, int batch, int num_kv_heads, int head_dim, int kv_capacity,
+              const int32_t* positions, int n_new, tq_quant_mode mode, int ring, void* stream,
+              const char* fn) {
   clear_error();
-  TQ_CHECK_ARG(valid_dtype(x_dtype), "tq_kv_append_int4: bad x_dtype");
+  TQ_CHECK_ARG(valid_dtype(x_dtype), "%s: bad x_dtype", fn);
   TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32,
-               "tq_kv_append_int4: sb_dtype must be f16 or f32");
-  TQ_CHECK_ARG(mode == TQ_QUANT_MLX || mode == TQ_QUANT_MINMAX, "tq_kv_append_int4: bad mode");
+               "%s: sb_dtype must be f16 or f32", fn);
+  TQ_CHECK_ARG(mode == TQ_QUANT_MLX || mode == TQ_QUANT_MINMAX, "%s: bad mode", fn);
   TQ_CHECK_ARG(head_dim > 0 && head_dim % 64 == 0 && head_dim <= 4096,
-               "tq_kv_append_int4: head_dim must be a multiple of 64 <= 4096");
+               "%s: head_dim must be a multiple of 64 <= 4096", fn);
   TQ_CHECK_ARG(batch >= 0 && num_kv_heads > 0 && n_new >= 0 && kv_capacity > 0,
-               "tq_kv_append_int4: bad sizes");
+               "%s: bad sizes", fn);
   if (batch == 0 || n_new == 0) return TQ_OK;
   TQ_CHECK_ARG(k_new && v_new && k_quant && k_scales && k_biases && v_quant && v_scales &&
                    v_biases && positions,
-               "tq_kv_append_int4: null pointer");
+               "%s: null pointer", fn);
   if (int r = check_align(k_new, 16, "k_new")) return r;
   if (int r = check_align(v_new, 16, "v_new")) return r;
   QuantParams p{};
@@ -236,7 +243,31 @@ extern "C" int tq_kv_append_int4(const void* k_new, const void* v_new, tq_dtype 
   p.heads = num_kv_heads;
   p.n_new = n_new;
   p.cap = kv_capacity;
+  p.ring = ring;
   return launch_quantize(p, 2, sb_dtype, static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+extern "C" int tq_kv_append_int4(const void* k_new, const void* v_new, tq_dtype x_dtype,
+                                 uint32_t* k_quant, void* k_scales, void* k_biases,
+                                 uint32_t* v_quant, void* v_scales, void* v_biases,
+                                 tq_dtype sb_dtype, int batch, int num_kv_heads, int head_dim,
+                                 int kv_capacity, const int32_t* positions, int n_new,
+                                 tq_quant_mode mode, void* stream) {
+  return kv_append(k_new, v_new, x_dtype, k_quant, k_scales, k_biases, v_quant, v_scales,
+                   v_biases, sb_dtype, batch, num_kv_heads, head_dim, kv_capacity, positions,
+                   n_new, mode, 0, stream, "tq_kv_append_int4");
+}
+
+extern "C" int tq_kv_append_int4_ring(const void* k_new, const void* v_new, tq_dtype x_dtype,
+                                      uint32_t* k_quant, void* k_scales, void* k_biases,
+                                      uint32_t* v_quant, void* v_scales, void* v_biases,
+                                      tq_dtype sb_dtype, int batch, int num_kv_heads,
+                                      int head_dim, int kv_capacity, const int32_t* positions,
+                                      int n_new, tq_quant_mode mode, void* stream) {
+  return kv_append(k_new, v_new, x_dtype, k_quant, k_scales, k_biases, v_quant, v_scales,
+                   v_biases, sb_dtype, batch, num_kv_heads, head_dim, kv_capacity, positions,
+                   n_new, mode, 1, stream, "tq_kv_append_int4_ring");
 }
 
 extern "C" int tq_dequantize_int4(const uint32_t* w_q, const void* scales, const void* biases,

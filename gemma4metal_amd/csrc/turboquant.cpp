@@ -260,21 +260,39 @@ array dequantize(const array& w, const array& scales, const array& biases, int g
   return out;
 }
 
-void kv_append_int4(const array& k_new, const array& v_new, array& k_quant, array& k_scales,
-                    array& k_biases, array& v_quant, array& v_scales, array& v_biases,
-                    const array& positions, StreamOrDevice s) {
+namespace {
+using AppendFn = int (*)(const void*, const void*, tq_dtype, uint32_t*, void*, void*, uint32_t*,
+                         void*, void*, tq_dtype, int, int, int, int, const int32_t*, int,
+                         tq_quant_mode, void*);
+void append_common(AppendFn fn, const char* what, const array& k_new, const array& v_new,
+                   array& k_quant, array& k_scales, array& k_biases, array& v_quant,
+                   array& v_scales, array& v_biases, const array& positions, StreamOrDevice s) {
   need(k_new.ndim() == 4 && v_new.shape() == k_new.shape(), "k_new / v_new must be (B, Hkv, T, D)");
   need(k_quant.ndim() == 4, "caches must be (B, Hkv, capacity, .)");
   need(positions.dtype() == Dtype::int32, "positions must be int32");
-  check(tq_kv_append_int4(k_new.data(), v_new.data(), c_dtype(k_new.dtype()),
-                          static_cast<uint32_t*>(k_quant.data()), k_scales.data(),
-                          k_biases.data(), static_cast<uint32_t*>(v_quant.data()),
-                          v_scales.data(), v_biases.data(), c_dtype(k_scales.dtype()),
-                          static_cast<int>(k_new.shape(0)), static_cast<int>(k_new.shape(1)),
-                          static_cast<int>(k_new.shape(3)), static_cast<int>(k_quant.shape(2)),
-                          static_cast<const int32_t*>(positions.data()),
-                          static_cast<int>(k_new.shape(2)), TQ_QUANT_MLX, s),
-        "kv_append_int4");
+  check(fn(k_new.data(), v_new.data(), c_dtype(k_new.dtype()),
+           static_cast<uint32_t*>(k_quant.data()), k_scales.data(), k_biases.data(),
+           static_cast<uint32_t*>(v_quant.data()), v_scales.data(), v_biases.data(),
+           c_dtype(k_scales.dtype()), static_cast<int>(k_new.shape(0)),
+           static_cast<int>(k_new.shape(1)), static_cast<int>(k_new.shape(3)),
+           static_cast<int>(k_quant.shape(2)), static_cast<const int32_t*>(positions.data()),
+           static_cast<int>(k_new.shape(2)), TQ_QUANT_MLX, s),
+        what);
+}
+}  // namespace
+
+void kv_append_int4(const array& k_new, const array& v_new, array& k_quant, array& k_scales,
+                    array& k_biases, array& v_quant, array& v_scales, array& v_biases,
+                    const array& positions, StreamOrDevice s) {
+  append_common(tq_kv_append_int4, "kv_append_int4", k_new, v_new, k_quant, k_scales, k_biases,
+                v_quant, v_scales, v_biases, positions, s);
+}
+
+void kv_append_int4_ring(const array& k_new, const array& v_new, array& k_quant,
+                         array& k_scales, array& k_biases, array& v_quant, array& v_scales,
+                         array& v_biases, const array& positions, StreamOrDevice s) {
+  append_common(tq_kv_append_int4_ring, "kv_append_int4_ring", k_new, v_new, k_quant, k_scales,
+                k_biases, v_quant, v_scales, v_biases, positions, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -199,12 +199,19 @@ def dequantize(w_q: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
 class Int4KVCache:
     """Preallocated int4 KV cache [B, Hkv, capacity, .] with per-sequence
     lengths on the device: the in-place replacement for the reference's
-    per-token ``concatenate`` (``engine/gemma4_multilayer.cpp:230-240``)."""
+    per-token ``concatenate`` (``engine/gemma4_multilayer.cpp:230-240``).
+
+    ``ring=True`` makes it the window eviction of a sliding layer (the
+    reference trims with ``slice``, ``engine/gemma4_multilayer.cpp:243-248``):
+    ``lengths`` count tokens seen, token i lives in row i mod capacity, and
+    attention covers the newest ``min(length, capacity)`` tokens -- exactly the
+    reference window rule with window = capacity."""
 
     def __init__(self, batch: int, num_kv_heads: int, capacity: int, head_dim: int,
-                 device, scale_dtype: torch.dtype = torch.float16):
+                 device, scale_dtype: torch.dtype = torch.float16, ring: bool = False):
         kw = dict(device=device)
         self.B, self.Hkv, self.cap, self.D = batch, num_kv_heads, capacity, head_dim
+        self.ring = bool(ring)
         self.kq = torch.zeros((batch, num_kv_heads, capacity, head_dim // 8), dtype=torch.uint32, **kw)
         self.vq = torch.zeros_like(self.kq)
         self.ks = torch.zeros((batch, num_kv_heads, capacity, head_dim // 64), dtype=scale_dtype, **kw)
@@ -218,14 +225,20 @@ class Int4KVCache:
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, *, mode: str = "mlx",
                advance: bool = True, stream=None):
-        """Quantize (B, Hkv, T, D) new rows into rows [len_b, len_b+T)."""
-        kv_append_int4(k_new, v_new, *self.tensors(), self.lengths, mode=mode, stream=stream)
+        """Quantize (B, Hkv, T, D) new rows into rows [len_b, len_b+T) (mod
+        capacity for a ring)."""
+        kv_append_int4(k_new, v_new, *self.tensors(), self.lengths, mode=mode, ring=self.ring,
+                       stream=stream)
         if advance:
             self.lengths += k_new.shape[2]
 
     def attend(self, queries: torch.Tensor, gqa_factor: int, scale: float = 1.0,
                sliding_window: int = 0, windows: Optional[torch.Tensor] = None,
                max_kv_len: Optional[int] = None, stream=None) -> torch.Tensor:
+        if self.ring:
+            # the ring is the window: every stored row is attended
+            _need(sliding_window == 0 and windows is None, "a ring cache takes no extra window")
+            _need(max_kv_len is None or max_kv_len == self.cap, "a ring attends its capacity")
         return sdpa_int4_ragged(queries, *self.tensors(), self.lengths, gqa_factor, scale,
                                 sliding_window, windows=windows, max_kv_len=max_kv_len,
                                 stream=stream)
@@ -234,9 +247,11 @@ class Int4KVCache:
 def kv_append_int4(k_new: torch.Tensor, v_new: torch.Tensor,
                    k_quant: torch.Tensor, k_scales: torch.Tensor, k_biases: torch.Tensor,
                    v_quant: torch.Tensor, v_scales: torch.Tensor, v_biases: torch.Tensor,
-                   positions: torch.Tensor, *, mode: str = "mlx", stream=None) -> None:
+                   positions: torch.Tensor, *, mode: str = "mlx", ring: bool = False,
+                   stream=None) -> None:
     """Quantize k_new / v_new (B, Hkv, T, D) and write them at rows
-    positions[b] .. positions[b]+T-1 of the (B, Hkv, cap, .) caches."""
+    positions[b] .. positions[b]+T-1 of the (B, Hkv, cap, .) caches (rows mod
+    cap, last cap tokens only, when ``ring``)."""
     for n, t in (("k_new", k_new), ("v_new", v_new), ("k_quant", k_quant),
                  ("k_scales", k_scales), ("k_biases", k_biases), ("v_quant", v_quant),
                  ("v_scales", v_scales), ("v_biases", v_biases), ("positions", positions)):
@@ -250,7 +265,8 @@ def kv_append_int4(k_new: torch.Tensor, v_new: torch.Tensor,
     cap = k_quant.shape[2]
     sbt = _sb_dtype("k_scales", k_scales)
     _need(positions.dtype == torch.int32 and positions.numel() == B, "positions must be int32 [B]")
-    call("tq_kv_append_int4", _ptr(k_new), _ptr(v_new), _DT[k_new.dtype], _ptr(k_quant),
+    call("tq_kv_append_int4_ring" if ring else "tq_kv_append_int4", _ptr(k_new), _ptr(v_new),
+         _DT[k_new.dtype], _ptr(k_quant),
          _ptr(k_scales), _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, B,
          Hkv, D, cap, _ptr(positions), T, _MODES[mode], _stream(stream))
 

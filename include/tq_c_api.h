@@ -86,8 +86,10 @@ int tq_sdpa_int4(const void* q, tq_dtype q_dtype,
 
 /* Batched ragged decode: sequence b attends rows [0, seq_lens[b]) of its cache
  * under window windows[b] (windows == NULL -> sliding_window for all).
- * seq_lens / windows are DEVICE int32 arrays of length batch; max_kv_len must
- * bound every seq_lens[b] (it sizes the launch grid).
+ * seq_lens / windows are DEVICE int32 arrays of length batch; max_kv_len
+ * (<= kv_capacity) sizes the launch grid, and a seq_lens[b] above it is
+ * clamped to it (a ring cache passes tokens seen, see
+ * tq_kv_append_int4_ring).
  *   q [batch, num_heads, head_dim]; caches [batch, num_kv_heads, kv_capacity, .];
  *   out [batch, num_heads, head_dim] f32.
  * The reference has no batch dimension (lib/turboquant.cpp:392,400); this is
@@ -124,6 +126,24 @@ int tq_kv_append_int4(const void* k_new, const void* v_new, tq_dtype x_dtype,
                       int batch, int num_kv_heads, int head_dim, int kv_capacity,
                       const int32_t* positions, int n_new, tq_quant_mode mode,
                       void* stream);
+
+/* tq_kv_append_int4_ring: the same quantize-and-store into a ring of
+ * kv_capacity rows per (sequence, kv head), the window eviction of a
+ * sliding-attention layer (the reference instead trims with `slice`,
+ * engine/gemma4_multilayer.cpp:243-248).  positions[b] >= 0 is the number of
+ * tokens sequence b has seen; token t of the append goes to row
+ * (positions[b] + t) mod kv_capacity, and of an append longer than the ring
+ * only its last kv_capacity tokens are stored.  The ring then holds exactly
+ * the keys the reference window rule keeps (lib/turboquant.metal:779) when
+ * kv_capacity equals the window; attend with tq_sdpa_int4_ragged, seq_lens =
+ * tokens seen, max_kv_len = kv_capacity (lengths are clamped to it) and
+ * window 0 -- attention does not depend on the order of the keys. */
+int tq_kv_append_int4_ring(const void* k_new, const void* v_new, tq_dtype x_dtype,
+                           uint32_t* k_quant, void* k_scales, void* k_biases,
+                           uint32_t* v_quant, void* v_scales, void* v_biases, tq_dtype sb_dtype,
+                           int batch, int num_kv_heads, int head_dim, int kv_capacity,
+                           const int32_t* positions, int n_new, tq_quant_mode mode,
+                           void* stream);
 
 /* Dequantize rows (for the engine's prefill fallback,
  * engine/gemma4_multilayer.cpp:307-308): out[r, d] = s*nibble + b as f32. */

@@ -105,6 +105,11 @@ array dequantize(const array& w, const array& scales, const array& biases, int g
 void kv_append_int4(const array& k_new, const array& v_new, array& k_quant, array& k_scales,
                     array& k_biases, array& v_quant, array& v_scales, array& v_biases,
                     const array& positions, StreamOrDevice s = {});
+// The same into rings of capacity rows (sliding-window eviction): token t
+// goes to row (positions[b] + t) mod capacity, positions[b] = tokens seen.
+void kv_append_int4_ring(const array& k_new, const array& v_new, array& k_quant,
+                         array& k_scales, array& k_biases, array& v_quant, array& v_scales,
+                         array& v_biases, const array& positions, StreamOrDevice s = {});
 
 // ---- PolarQuant (lib/turboquant.h:52-165) -----------------------------------
 // Reference layouts: 16-value blocks, 4 levels, codebooks per level.

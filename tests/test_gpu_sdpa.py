@@ -224,3 +224,52 @@ def test_sdpa_global_layer_full_context(gpu):
         c = [host(t[sl]) for t in (kq, ks, kb, vq, vs, vb)]
         ref = coracle.sdpa_int4_f64(qv[8 * kvh:8 * kvh + 8], *c, 8)
         assert_close(out[8 * kvh:8 * kvh + 8], ref, f"global L=32768 kv head {kvh}")
+
+
+def test_ring_cache_equals_window_rule(gpu):
+    """Sliding-window eviction by a ring of capacity W: after appends that
+    wrap the ring (a prefill longer than W, single tokens, a 3-token step),
+    attention over the ring (window 0) equals the reference window rule W
+    over the full history (lib/turboquant.metal:779)."""
+    rng = np.random.default_rng(61)
+    B, Hq, Hkv, D, W = 2, 32, 16, 256, 64
+    ring = gpu.Int4KVCache(B, Hkv, W, D, "cuda", ring=True)
+    hist_k = np.zeros((B, Hkv, 0, D), np.float32)
+    hist_v = np.zeros((B, Hkv, 0, D), np.float32)
+    for T in (70, 1, 1, 3, 1):
+        k = O.rms_norm(rng.standard_normal((B, Hkv, T, D)).astype(np.float32))
+        v = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+        ring.append(dev(k), dev(v))
+        hist_k = np.concatenate([hist_k, k], axis=2)
+        hist_v = np.concatenate([hist_v, v], axis=2)
+        qd, qv = queries(rng, (B, Hq, D), "bf16")
+        out = ring.attend(qd, Hq // Hkv)
+        n = hist_k.shape[2]
+        c = O.quantize_int4(hist_k) + O.quantize_int4(hist_v)
+        ref = O.sdpa_int4_ragged(qv, *c, np.full(B, n, np.int32), np.full(B, W, np.int32), Hq // Hkv)
+        assert_close(host(out), ref, f"ring after {n} tokens")
+    assert np.all(host(ring.lengths) == hist_k.shape[2])
+
+
+def test_prompt_cache_file_round_trip(gpu, tmp_path):
+    """save_kv_cache / load_kv_cache (reference prompt-cache layout) with GPU
+    caches: a global (linear) and a sliding (ring) layer reload into fresh
+    caches whose attention output is bit-identical."""
+    from gemma4metal_amd import kvcache_io as IO
+    rng = np.random.default_rng(71)
+    Hq, Hkv, D = 32, 16, 256
+    lin = gpu.Int4KVCache(1, Hkv, 300, D, "cuda")
+    ring = gpu.Int4KVCache(1, Hkv, 128, D, "cuda", ring=True)
+    for T in (150, 1, 2):
+        k = dev(O.rms_norm(rng.standard_normal((1, Hkv, T, D)).astype(np.float32)))
+        v = dev(rng.standard_normal((1, Hkv, T, D)).astype(np.float32))
+        lin.append(k, v)
+        ring.append(k, v)
+    p = str(tmp_path / "kv.safetensors")
+    IO.save_kv_cache(p, [lin, ring], cache_offset=153)
+    lin2 = gpu.Int4KVCache(1, Hkv, 300, D, "cuda")
+    ring2 = gpu.Int4KVCache(1, Hkv, 128, D, "cuda", ring=True)
+    assert IO.load_kv_cache(p, [lin2, ring2]) == 153
+    qd, _ = queries(rng, (1, Hq, D), "bf16")
+    for a, b in ((lin, lin2), (ring, ring2)):
+        assert np.array_equal(host(a.attend(qd, 2)), host(b.attend(qd, 2)))
