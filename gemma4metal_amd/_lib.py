@@ -41,6 +41,8 @@ SIGNATURES = {
     "tq_sdpa_int4": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, I, F, I, P, SZ, P]),
     "tq_sdpa_int4_ragged": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, P, P, I, I, F, I,
                                 P, SZ, P]),
+    "tq_sdpa_int4_prefill": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, I, I, F, I, P, SZ,
+                                 P]),
     "tq_quantize_int4": (I, [P, I, I64, I, I, I, I, P, P, P, I, P]),
     "tq_kv_append_int4": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, P, I, I, P]),
     "tq_kv_append_int4_ring": (I, [P, P, I, P, P, P, P, P, P, I, I, I, I, I, P, I, I, P]),

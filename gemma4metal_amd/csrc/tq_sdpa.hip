@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
   if (split >= rg.S) return;
   const int S = rg.S, t_begin = rg.t_begin, t_end = rg.t_end;
 
-  const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
+  const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
   const uint32_t* kq = p.kq + row0 * RW + j * WPL;
   const uint32_t* vq = p.vq + row0 * RW + j * WPL;
   const SB* ks = static_cast<const SB*>(p.ks) + row0 * NG + grp;
@@ -380,7 +380,8 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
                 const uint32_t* vq, const void* vs, const void* vb, int sb_dtype, float* out,
                 int batch, int Hq, int Hkv, int D, int cap, int n, const int32_t* seq_lens,
                 const int32_t* windows, int max_len, int gqa, float scale, int window,
-                void* workspace, size_t ws_bytes, void* stream, const char* fn) {
+                void* workspace, size_t ws_bytes, void* stream, const char* fn,
+                int prefill = 0) {
   TQ_CHECK_ARG(valid_dtype(q_dtype), "%s: bad q_dtype %d", fn, q_dtype);
   TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32, "%s: sb_dtype must be f16 or f32", fn);
   if (D != 128 && D != 256 && D != 512) {
@@ -417,8 +418,10 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
   int eff_len = max_len;
   if (!seq_lens && window > 0) eff_len = std::min(max_len, window);
-  const int chunk = plan_chunk(eff_len, groups, min_splits_for(batch));
-  const int max_splits = max_splits_bound(eff_len, groups, min_splits_for(batch));
+  // (a prefill's queries are many short-to-long sequences: no minimum split)
+  const int min_splits = prefill ? 1 : min_splits_for(batch);
+  const int chunk = plan_chunk(eff_len, groups, min_splits);
+  const int max_splits = max_splits_bound(eff_len, groups, min_splits);
   const WsLayout wl = ws_layout(batch, Hq, D, max_splits);
   if (max_splits > 1) {
     if (!workspace || ws_bytes < wl.total) {
@@ -427,8 +430,9 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
     }
   }
   TQ_CHECK_ARG(Hkv * n_sub <= 65535 && batch <= 65535, "%s: grid too large", fn);
-  TQ_CHECK_ARG(static_cast<int64_t>(batch) * Hq <= kMaxCounters,
-               "%s: batch * num_heads must be <= %lld", fn, static_cast<long long>(kMaxCounters));
+  TQ_CHECK_ARG(static_cast<int64_t>(batch) * Hq <= kMaxCounters || (prefill && max_splits == 1),
+               "%s: batch (queries) * num_heads must be <= %lld", fn,
+               static_cast<long long>(kMaxCounters));
 
   SdpaParams p{};
   p.q = q;
@@ -441,7 +445,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   p.ws_ml = ws ? reinterpret_cast<float*>(ws + wl.ml_off) : nullptr;
   p.ws_o = ws ? reinterpret_cast<float*>(ws + wl.o_off) : nullptr;
   p.Hq = Hq; p.Hkv = Hkv; p.cap = cap; p.gqa = gqa; p.n_sub = n_sub;
-  p.n = max_len;
+  p.n = prefill ? n : max_len;  // prefill: positions before the first query
   p.seq_lens = seq_lens;
   p.windows = windows;
   p.window = window;
@@ -449,6 +453,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   p.scale_log2 = scale * 1.4426950408889634f;
   p.chunk = chunk;
   p.max_splits = max_splits;
+  p.prefill = prefill;
 
   dim3 grid(max_splits, Hkv * n_sub, batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -513,4 +518,26 @@ extern "C" int tq_sdpa_int4_ragged(const void* q, tq_dtype q_dtype, const uint32
                      sb_dtype, out, batch, num_heads, num_kv_heads, head_dim, kv_capacity,
                      max_kv_len, seq_lens, windows, max_kv_len, gqa_factor, scale,
                      sliding_window, workspace, workspace_bytes, stream, "tq_sdpa_int4_ragged");
+}
+
+extern "C" int tq_sdpa_int4_prefill(const void* q, tq_dtype q_dtype, const uint32_t* k_quant,
+                                    const void* k_scales, const void* k_biases,
+                                    const uint32_t* v_quant, const void* v_scales,
+                                    const void* v_biases, tq_dtype sb_dtype, float* out,
+                                    int num_heads, int num_kv_heads, int head_dim, int n_prior,
+                                    int n_new, int kv_capacity, int gqa_factor, float scale,
+                                    int sliding_window, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  clear_error();
+  const char* fn = "tq_sdpa_int4_prefill";
+  TQ_CHECK_ARG(n_prior >= 0 && n_new >= 0, "%s: n_prior and n_new must be >= 0", fn);
+  TQ_CHECK_ARG(static_cast<int64_t>(n_prior) + n_new <= kv_capacity,
+               "%s: n_prior + n_new (%d + %d) exceeds kv_capacity %d", fn, n_prior, n_new,
+               kv_capacity);
+  if (n_new == 0) return TQ_OK;
+  TQ_CHECK_ARG(n_new <= 65535, "%s: at most 65535 queries per call", fn);
+  return sdpa_common(q, q_dtype, k_quant, k_scales, k_biases, v_quant, v_scales, v_biases,
+                     sb_dtype, out, n_new, num_heads, num_kv_heads, head_dim, kv_capacity,
+                     n_prior, nullptr, nullptr, n_prior + n_new, gqa_factor, scale,
+                     sliding_window, workspace, workspace_bytes, stream, fn, 1);
 }

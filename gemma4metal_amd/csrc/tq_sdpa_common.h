@@ -44,7 +44,14 @@ struct SdpaParams {
   // 0: the last workgroup of a split sequence merges the partials; 1: the
   // kernel only writes them and launch_merge_splits merges them afterwards.
   int ext_merge;
+  // Prefill: batch element b is the query at position n + b over the one
+  // cache of batch 0, attending its first n + b + 1 rows (causal), under
+  // `window` (engine/gemma4_multilayer.cpp:349-358).
+  int prefill;
 };
+
+// Batch index of the cache that batch element b reads.
+__device__ __forceinline__ int cache_batch(const SdpaParams& p, int b) { return p.prefill ? 0 : b; }
 
 // The keys one workgroup attends: rows [t_begin, t_end) of its sequence's
 // cache.  Key ki survives the reference window rule (skip ki when
@@ -56,7 +63,7 @@ struct SplitRange {
 };
 
 __device__ __forceinline__ SplitRange split_range(const SdpaParams& p, int b, int split) {
-  int n_b = p.seq_lens ? p.seq_lens[b] : p.n;
+  int n_b = p.prefill ? p.n + b + 1 : (p.seq_lens ? p.seq_lens[b] : p.n);
   n_b = min(n_b, p.n_clamp);
   const int W = p.windows ? p.windows[b] : p.window;
   const int lo = W > 0 ? max(0, n_b - W) : 0;

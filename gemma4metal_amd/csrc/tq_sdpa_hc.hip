@@ -116,7 +116,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   __shared__ float sh_qhat[G][NG];
   __shared__ int sh_F[G];
 
-  const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
+  const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
   const char* kq_rows = reinterpret_cast<const char*>(p.kq + row0 * (D / 8));
   const char* vq_rows = reinterpret_cast<const char*>(p.vq + row0 * (D / 8));
   // lane group c loads scale array c: k scale, k bias, v scale, v bias

@@ -186,7 +186,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   __shared__ int sh_F[G];
 
   // ---- first loads, issued before the prologue to overlap its latency ------
-  const int64_t row0 = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.cap;
+  const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
   const uint32_t* kq_row0 = p.kq + row0 * RW;
   const uint32_t* vq_row0 = p.vq + row0 * RW;
   // (a select chain over kernel-argument pointers keeps the global address

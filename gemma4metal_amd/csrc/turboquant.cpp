@@ -224,6 +224,28 @@ array sdpa_int4_ragged(const array& queries, const array& k_quant, const array& 
   return out;
 }
 
+array sdpa_int4_prefill(const array& queries, const array& k_quant, const array& k_scales,
+                        const array& k_biases, const array& v_quant, const array& v_scales,
+                        const array& v_biases, int n_prior, int gqa_factor, float scale,
+                        int sliding_window, StreamOrDevice s) {
+  need(queries.ndim() == 3 && k_quant.ndim() == 3, "queries (n_new, Hq, D), caches (Hkv, cap, .)");
+  const int S = static_cast<int>(queries.shape(0)), Hq = static_cast<int>(queries.shape(1));
+  const int D = static_cast<int>(queries.shape(2));
+  const int Hkv = static_cast<int>(k_quant.shape(0)), cap = static_cast<int>(k_quant.shape(1));
+  need(is_sb(k_scales.dtype()), "scales must be float32 or float16");
+  array out = array::empty({S, Hq, D}, Dtype::float32);
+  size_t have = 0;
+  void* ws = workspace(tq_sdpa_int4_workspace_size(S > 0 ? S : 1, Hq, Hkv, D, n_prior + S), &have);
+  check(tq_sdpa_int4_prefill(queries.data(), c_dtype(queries.dtype()),
+                             static_cast<const uint32_t*>(k_quant.data()), k_scales.data(),
+                             k_biases.data(), static_cast<const uint32_t*>(v_quant.data()),
+                             v_scales.data(), v_biases.data(), c_dtype(k_scales.dtype()),
+                             static_cast<float*>(out.data()), Hq, Hkv, D, n_prior, S, cap,
+                             gqa_factor, scale, sliding_window, ws, have, s),
+        "sdpa_int4_prefill");
+  return out;
+}
+
 std::vector<array> quantize(const array& x, int group_size, int bits, Dtype scale_dtype,
                             StreamOrDevice s) {
   need(x.ndim() >= 1, "x must have a last axis");

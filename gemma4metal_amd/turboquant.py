@@ -111,6 +111,47 @@ def sdpa_int4(queries: torch.Tensor,
     return out
 
 
+def sdpa_int4_prefill(queries: torch.Tensor,
+                      k_quant: torch.Tensor, k_scales: torch.Tensor, k_biases: torch.Tensor,
+                      v_quant: torch.Tensor, v_scales: torch.Tensor, v_biases: torch.Tensor,
+                      n_prior: int, gqa_factor: int, scale: float = 1.0,
+                      sliding_window: int = 0, *, out: Optional[torch.Tensor] = None,
+                      stream=None) -> torch.Tensor:
+    """Multi-query (prefill) attention of the reference's fallback path
+    (``engine/gemma4_multilayer.cpp:343-364``): queries (n_new, num_heads,
+    head_dim) at positions n_prior .. n_prior+n_new-1 over rows
+    [0, n_prior + n_new) of the (num_kv_heads, capacity, .) caches (the new
+    rows already appended); query i sees key j iff j <= n_prior + i and, with a
+    window W > 0, n_prior + i - j < W.  Returns (n_new, num_heads, head_dim)
+    float32."""
+    for n, t in (("queries", queries), ("k_quant", k_quant), ("k_scales", k_scales),
+                 ("k_biases", k_biases), ("v_quant", v_quant), ("v_scales", v_scales),
+                 ("v_biases", v_biases)):
+        _check_cuda(n, t)
+    _need(queries.dim() == 3 and queries.dtype in _DT, "queries must be (n_new, Hq, D)")
+    S, Hq, D = queries.shape
+    _need(k_quant.dim() == 3 and k_quant.dtype in _QUANT_DT, "k_quant must be (Hkv, cap, D/8) uint32")
+    Hkv, cap, _ = k_quant.shape
+    for n, t in (("k_quant", k_quant), ("v_quant", v_quant)):
+        _need(t.shape == (Hkv, cap, D // 8), f"{n} must be ({Hkv}, {cap}, {D // 8})")
+    sbt = _sb_dtype("k_scales", k_scales)
+    for n, t in (("k_scales", k_scales), ("k_biases", k_biases), ("v_scales", v_scales),
+                 ("v_biases", v_biases)):
+        _need(t.shape == (Hkv, cap, D // 64) and _DT.get(t.dtype) == sbt,
+              f"{n} must be ({Hkv}, {cap}, {D // 64}) of one scale dtype")
+    if out is None:
+        out = torch.empty((S, Hq, D), dtype=torch.float32, device=queries.device)
+    _check_cuda("out", out)
+    _need(out.shape == (S, Hq, D) and out.dtype == torch.float32, "out must be (n_new, Hq, D) f32")
+    nbytes = _lib.load().tq_sdpa_int4_workspace_size(max(S, 1), Hq, Hkv, D, int(n_prior) + S)
+    ws = workspace(nbytes, queries.device)
+    call("tq_sdpa_int4_prefill", _ptr(queries), _DT[queries.dtype], _ptr(k_quant), _ptr(k_scales),
+         _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out), Hq, Hkv,
+         D, int(n_prior), S, cap, int(gqa_factor), float(scale), int(sliding_window), _ptr(ws),
+         ws.numel(), _stream(stream))
+    return out
+
+
 def sdpa_int4_ragged(queries: torch.Tensor,
                      k_quant: torch.Tensor, k_scales: torch.Tensor, k_biases: torch.Tensor,
                      v_quant: torch.Tensor, v_scales: torch.Tensor, v_biases: torch.Tensor,

@@ -103,6 +103,25 @@ int tq_sdpa_int4_ragged(const void* q, tq_dtype q_dtype,
                         int max_kv_len, int gqa_factor, float scale, int sliding_window,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Multi-query (prefill) attention over one cache: the n_new queries
+ * q [n_new, num_heads, head_dim] at positions n_prior .. n_prior+n_new-1
+ * attend rows [0, n_prior + n_new) of the [num_kv_heads, kv_capacity, .]
+ * caches, which must already hold the new rows.  Query i sees key j iff
+ * j <= n_prior + i and, for sliding_window > 0, n_prior + i - j <
+ * sliding_window: the mask of the reference's prefill fallback
+ * (engine/gemma4_multilayer.cpp:343-364, dequantize + masked
+ * scaled_dot_product_attention).  out [n_new, num_heads, head_dim] f32.
+ * Workspace: tq_sdpa_int4_workspace_size(n_new, num_heads, num_kv_heads,
+ * head_dim, n_prior + n_new) bytes (zero-filled once, as for decode). */
+int tq_sdpa_int4_prefill(const void* q, tq_dtype q_dtype,
+                         const uint32_t* k_quant, const void* k_scales, const void* k_biases,
+                         const uint32_t* v_quant, const void* v_scales, const void* v_biases,
+                         tq_dtype sb_dtype, float* out,
+                         int num_heads, int num_kv_heads, int head_dim,
+                         int n_prior, int n_new, int kv_capacity,
+                         int gqa_factor, float scale, int sliding_window,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- quantize / append ----------------------------------------------------
  * tq_quantize_int4 replaces MLX quantize(x, 64, 4) as called at
  * engine/gemma4_multilayer.cpp:228-229: rows x dim values of x (x_dtype) ->

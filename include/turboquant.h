@@ -91,6 +91,17 @@ array sdpa_int4_ragged(const array& queries, const array& k_quant, const array& 
                        float scale = 1.0f, int sliding_window = 0, const array& windows = {},
                        StreamOrDevice s = {});
 
+// Multi-query (prefill) attention of the engine's fallback path
+// (engine/gemma4_multilayer.cpp:343-364): queries (n_new, num_heads,
+// head_dim) at positions n_prior .. n_prior+n_new-1 over rows
+// [0, n_prior + n_new) of caches (num_kv_heads, capacity, .) that already
+// hold the new rows; causal, and sliding_window > 0 limits each query to its
+// last sliding_window keys.  Returns (n_new, num_heads, head_dim) f32.
+array sdpa_int4_prefill(const array& queries, const array& k_quant, const array& k_scales,
+                        const array& k_biases, const array& v_quant, const array& v_scales,
+                        const array& v_biases, int n_prior, int gqa_factor, float scale = 1.0f,
+                        int sliding_window = 0, StreamOrDevice s = {});
+
 // ---- quantize / append (MLX quantize(x, 64, 4) at
 // engine/gemma4_multilayer.cpp:228-229) --------------------------------------
 // Returns {w_q uint32 (..., D/8), scales (..., D/64), biases (..., D/64)} with

@@ -218,6 +218,39 @@ def sdpa_int4_ragged(q, kq, ks, kb, vq, vs, vb, seq_lens, windows, gqa_factor: i
         for b in range(B)])
 
 
+def sdpa_int4_prefill(q, kq, ks, kb, vq, vs, vb, n_prior: int, gqa_factor: int,
+                      scale: float = 1.0, sliding_window: int = 0) -> np.ndarray:
+    """The engine's prefill fallback (``engine/gemma4_multilayer.cpp:
+    343-364``) in float64: dequantize the cache (``:307-308``), build the
+    additive mask md[i, j] = -1e9 where key j is in the future of query i
+    (j > n_prior + i) or, with a window, outside it (n_prior + i - j >= W)
+    (``:349-358``), then softmax(scale * q K^T + md) V per head with the kv
+    head h // gqa (MLX's GQA broadcast).
+
+    q: (n_new, Hq, D); caches (Hkv, cap, .) holding rows [0, n_prior+n_new).
+    Returns (n_new, Hq, D) float64."""
+    q = np.asarray(q, dtype=np.float64)
+    scale = float(np.float32(scale))
+    S, Hq, D = q.shape
+    L = n_prior + S
+    qpos = n_prior + np.arange(S)[:, None]
+    j = np.arange(L)[None, :]
+    masked = j > qpos
+    if sliding_window > 0:
+        masked |= (qpos - j) >= sliding_window
+    md = np.where(masked, -1e9, 0.0)
+    out = np.zeros((S, Hq, D), dtype=np.float64)
+    for kvh in range(kq.shape[0]):
+        K = dequantize(kq[kvh, :L], ks[kvh, :L], kb[kvh, :L])
+        V = dequantize(vq[kvh, :L], vs[kvh, :L], vb[kvh, :L])
+        for h in range(kvh * gqa_factor, (kvh + 1) * gqa_factor):
+            z = scale * (q[:, h, :] @ K.T) + md
+            z -= z.max(axis=1, keepdims=True)
+            w = np.exp(z)
+            out[:, h, :] = (w @ V) / w.sum(axis=1, keepdims=True)
+    return out
+
+
 def kv_append_int4(cache: dict, k_new: np.ndarray, v_new: np.ndarray, positions,
                    sb_dtype: str = "f16", mode: str = "mlx") -> None:
     """Quantize ``k_new``/``v_new`` (B, Hkv, T, D) and write them in place at

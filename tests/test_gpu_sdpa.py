@@ -273,3 +273,22 @@ def test_prompt_cache_file_round_trip(gpu, tmp_path):
     qd, _ = queries(rng, (1, Hq, D), "bf16")
     for a, b in ((lin, lin2), (ring, ring2)):
         assert np.array_equal(host(a.attend(qd, 2)), host(b.attend(qd, 2)))
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,prior,W,qdt", [
+    (32, 16, 256, 100, 0, 0, "bf16"),      # first prefill chunk, causal only
+    (32, 16, 256, 64, 700, 128, "bf16"),   # chunk after a cached prefix, sliding window
+    (32, 4, 512, 48, 300, 0, "bf16"),      # Gemma global layer (heads-as-columns kernel)
+    (8, 2, 128, 33, 5, 16, "f32"),
+    (4, 4, 256, 1, 90, 0, "f16"),          # a single query = decode
+])
+def test_sdpa_prefill_matches_oracle(gpu, Hq, Hkv, D, S, prior, W, qdt):
+    """Multi-query attention with the engine fallback's causal + window mask
+    (engine/gemma4_multilayer.cpp:343-364)."""
+    rng = np.random.default_rng(S * 13 + prior + D)
+    cap = prior + S + 7
+    qd, qv = queries(rng, (S, Hq, D), qdt)
+    c = host_cache(rng, Hkv, cap, D, "f16")
+    out = gpu.sdpa_int4_prefill(qd, *[dev(a) for a in c], prior, Hq // Hkv, 1.0, W)
+    ref = O.sdpa_int4_prefill(qv, *c, prior, Hq // Hkv, 1.0, W)
+    assert_close(host(out), ref, f"prefill S{S} prior{prior} W{W} D{D}")

@@ -163,3 +163,57 @@ def test_planted_mistakes_fail_library_check(mutation):
     ref = torch_reference(q, cache, 2, 1.0, 0, 24)
     assert np.max(np.abs(_mutant_sdpa(q, cache, 2, mutation) - ref)) > 1e-2
     assert np.max(np.abs(_mutant_sdpa(q, cache, 2, "none") - ref)) < 1e-10
+
+
+def prefill_case(seed, S, prior, Hq, Hkv, D):
+    rng = np.random.default_rng(seed)
+    q = O.rms_norm(rng.standard_normal((S, Hq, D)).astype(np.float32))
+    k = O.rms_norm(rng.standard_normal((Hkv, prior + S, D)).astype(np.float32))
+    v = rng.standard_normal((Hkv, prior + S, D)).astype(np.float32)
+    return q, O.quantize_int4(k) + O.quantize_int4(v)
+
+
+def test_prefill_oracle_is_torch_causal_attention():
+    """n_prior = 0, no window: exactly torch's is_causal attention (a library
+    routine) over the dequantized cache, GQA by repeating kv heads."""
+    S, Hq, Hkv, D = 40, 8, 2, 128
+    q, cache = prefill_case(5, S, 0, Hq, Hkv, D)
+    got = O.sdpa_int4_prefill(q, *cache, 0, Hq // Hkv, 0.7)
+    kq, ks, kb, vq, vs, vb = cache
+    K = torch.from_numpy(O.dequantize(kq, ks, kb)).repeat_interleave(Hq // Hkv, 0)[None]
+    V = torch.from_numpy(O.dequantize(vq, vs, vb)).repeat_interleave(Hq // Hkv, 0)[None]
+    Q = torch.from_numpy(np.asarray(q, np.float64)).permute(1, 0, 2)[None]
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        Q.contiguous(), K.contiguous(), V.contiguous(), is_causal=True, scale=float(np.float32(0.7)))
+    np.testing.assert_allclose(got, ref[0].permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("S,prior,W", [(24, 50, 0), (24, 50, 16), (1, 70, 0), (9, 0, 4)])
+def test_prefill_oracle_equals_per_query_decode(S, prior, W):
+    """Query i of a prefill is the decode of a sequence of n_prior + i + 1
+    keys under the same window (the decode oracle is pinned above)."""
+    Hq, Hkv, D = 4, 2, 256
+    q, cache = prefill_case(S + prior + W, S, prior, Hq, Hkv, D)
+    got = O.sdpa_int4_prefill(q, *cache, prior, 2, 1.0, W)
+    for i in range(S):
+        ref = O.sdpa_int4(q[i], *cache, 2, 1.0, W, kv_len=prior + i + 1)
+        np.testing.assert_allclose(got[i], ref, rtol=1e-10, atol=1e-10)
+
+
+def test_prefill_oracle_catches_planted_causal_off_by_one(monkeypatch):
+    """A mask that also hides the query's own key (j >= pos instead of
+    j > pos) must fail the per-query decode comparison."""
+    S, prior = 6, 10
+    q, cache = prefill_case(9, S, prior, 2, 1, 128)
+    real = np.where
+
+    def shifted(cond, a, b):
+        if isinstance(cond, np.ndarray) and cond.ndim == 2 and cond.shape == (S, prior + S):
+            pos = prior + np.arange(S)[:, None]
+            cond = cond | (np.arange(prior + S)[None, :] == pos)
+        return real(cond, a, b)
+    monkeypatch.setattr(O.np, "where", shifted)
+    bad = O.sdpa_int4_prefill(q, *cache, prior, 2)
+    monkeypatch.undo()
+    ref = np.stack([O.sdpa_int4(q[i], *cache, 2, kv_len=prior + i + 1) for i in range(S)])
+    assert np.abs(bad - ref).max() > 1e-3
