@@ -49,7 +49,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sets", type=int, default=8, help="distinct KV sets rotated")
     ap.add_argument("--workload", default="ctx32k",
-                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar", "global"])
+                    choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar", "global",
+                             "prefill"])
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -234,6 +235,31 @@ def main():
 
     if args.workload == "polar":
         bench_polar(args, torch, gen)
+        return
+
+    if args.workload == "prefill":
+        # chunked prefill through the engine's fallback attention
+        # (engine/gemma4_multilayer.cpp:343-364): n_new queries after n_prior
+        # cached positions, the new rows already appended
+        prior, S = 3584, 512
+        for label, Hq_, Hkv_, D_, W in (("sliding layer", 32, 16, 256, 1024),
+                                         ("global layer", 32, 4, 512, 0)):
+            L = prior + S
+            cache = gen_cache(tq, torch, Hkv_, L, D_, gen)
+            q = gen_q(torch, (S, Hq_, D_), gen)
+            out = torch.empty((S, Hq_, D_), dtype=torch.float32, device="cuda")
+            ms, _, _ = time_launches(torch, lambda i: tq.sdpa_int4_prefill(
+                q, *cache, prior, Hq_ // Hkv_, 1.0, W, out=out), args.steps, args.warmup)
+            keys = sum(min(prior + i + 1, W) if W else prior + i + 1 for i in range(S))
+            tflops = 4.0 * keys * D_ * Hq_ / (ms * 1e-3) / 1e12   # q.k and p.v, 2 flops per MAC
+            emit({"metric": f"int4-KV prefill attention TFLOP/s, {label}",
+                  "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+                  "warmup": args.warmup, "ms_per_step": round(ms, 5),
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                  "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
+                  "config": {"workload": f"prefill n_new={S} n_prior={prior} Hq={Hq_} Hkv={Hkv_} "
+                                         f"D={D_} W={W}", "global_batch": 1, "seq_len": L,
+                             "parallelism": "none (1 GPU)"}}, args)
         return
 
     if args.workload == "global":
