@@ -416,8 +416,17 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   if (try_mfma && D == 512 && sb_dtype == TQ_F16 && !hc) G = gqa % 2 == 0 ? 2 : 1;
   const int n_sub = gqa / G;
   const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
+  // Prefill on the matrix-core kernel: pq consecutive queries share a
+  // workgroup (its G * pq column sets fill the 16 MFMA columns), so each K/V
+  // byte serves pq queries.  Split planning stays per query, and a group's
+  // key range is the union of its windows (at most window + pq - 1 keys).
+  int pq = 1;
+  if (prefill && try_mfma && !hc && sb_dtype == TQ_F16) {
+    const int max_cols = D == 128 ? 8 : (D == 256 ? 4 : 2);  // G * pq the kernel serves
+    while (G * pq * 2 <= max_cols && pq * 2 <= batch) pq *= 2;
+  }
   int eff_len = max_len;
-  if (!seq_lens && window > 0) eff_len = std::min(max_len, window);
+  if (!seq_lens && window > 0) eff_len = std::min(max_len, window + pq - 1);
   // (a prefill's queries are many short-to-long sequences: no minimum split)
   const int min_splits = prefill ? 1 : min_splits_for(batch);
   const int chunk = plan_chunk(eff_len, groups, min_splits);
@@ -454,8 +463,10 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   p.chunk = chunk;
   p.max_splits = max_splits;
   p.prefill = prefill;
+  p.pq = pq;
+  p.nq = batch;
 
-  dim3 grid(max_splits, Hkv * n_sub, batch);
+  dim3 grid(max_splits, Hkv * n_sub, (batch + pq - 1) / pq);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (hc) {
     // 8 heads x 512 dims of partials per split: merged by a separate,
@@ -466,7 +477,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
     return launch_merge_splits(p, D, batch, s);
   }
   if (try_mfma) {
-    const int r = launch_sdpa_mfma(p, D, G, sb_dtype, grid, s);
+    const int r = launch_sdpa_mfma(p, D, G * pq, sb_dtype, grid, s);
     if (r >= 0) return r;
   }
   switch (D) {

@@ -48,6 +48,10 @@ struct SdpaParams {
   // cache of batch 0, attending its first n + b + 1 rows (causal), under
   // `window` (engine/gemma4_multilayer.cpp:349-358).
   int prefill;
+  // Prefill on the matrix-core kernel: each workgroup takes pq consecutive
+  // queries (grid z = query groups) of its heads, nq queries in all.
+  int pq;
+  int nq;
 };
 
 // Batch index of the cache that batch element b reads.
@@ -72,6 +76,19 @@ __device__ __forceinline__ SplitRange split_range(const SdpaParams& p, int b, in
   r.S = L > 0 ? (L + p.chunk - 1) / p.chunk : 1;
   r.t_begin = lo + split * p.chunk;
   r.t_end = min(r.t_begin + p.chunk, n_b);
+  return r;
+}
+
+// Key range of the prefill query group b0 .. b_last (positions n + b0 ..):
+// the union of their causal windows, cut into chunks as split_range does.
+__device__ __forceinline__ SplitRange prefill_range(const SdpaParams& p, int b0, int b_last,
+                                                    int split) {
+  const int lo = p.window > 0 ? max(0, p.n + b0 + 1 - p.window) : 0;
+  const int hi = p.n + b_last + 1;
+  SplitRange r;
+  r.S = (hi - lo + p.chunk - 1) / p.chunk;
+  r.t_begin = lo + split * p.chunk;
+  r.t_end = min(r.t_begin + p.chunk, hi);
   return r;
 }
 
@@ -147,12 +164,17 @@ struct Finalize {
 
   // Called by all threads after every wave stored its unnormalised output
   // O[h][d] (relative to its running max m[h]) and denominator l[h] into the
-  // arena (no barrier needed before the call).  head_base = b*Hq + first head.
+  // arena (no barrier needed before the call).  Column h is output row
+  // head_base + (h / gh) * qstride + h % gh (decode: head_base = b*Hq + first
+  // head, rows head_base + h); columns h >= nvalid are dropped.
   __device__ static void run(const SdpaParams& p, float* arena, int64_t head_base, int S,
-                             int split, int counter) {
+                             int split, int counter, int gh = G, int64_t qstride = 0,
+                             int nvalid = G) {
+    auto row = [&](int h) -> int64_t { return head_base + (h / gh) * qstride + h % gh; };
     __syncthreads();
     for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
       const int h = idx / D, d = idx - (idx / D) * D;
+      if (h >= nvalid) continue;
       float M = -INFINITY;
 #pragma unroll
       for (int w = 0; w < NW; ++w) M = fmaxf(M, m(arena, w)[h]);
@@ -164,9 +186,9 @@ struct Finalize {
         Ls += l(arena, w)[h] * f;
       }
       if (S == 1) {
-        p.out[(head_base + h) * D + d] = normalise(O, Ls, p.denom_eps);
+        p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
       } else {
-        const int64_t slot = (head_base + h) * p.max_splits + split;
+        const int64_t slot = row(h) * p.max_splits + split;
         store_coherent(p.ws_o + slot * D + d, O);
         if (d == 0) {
           store_coherent(p.ws_ml + slot * 2, M);
@@ -203,18 +225,20 @@ struct Finalize {
     float* s_l = arena + G * kMaxSplits;
     for (int i = threadIdx.x; i < G * S; i += kNT) {
       const int h = i / S, sp = i - (i / S) * S;
-      const int64_t slot = (head_base + h) * p.max_splits + sp;
+      if (h >= nvalid) continue;
+      const int64_t slot = row(h) * p.max_splits + sp;
       s_m[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2);
       s_l[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2 + 1);
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
       const int h = idx / D, d = idx - (idx / D) * D;
+      if (h >= nvalid) continue;
       const float* ms = s_m + h * kMaxSplits;
       const float* ls = s_l + h * kMaxSplits;
       float M = -INFINITY;
       for (int sp = 0; sp < S; ++sp) M = fmaxf(M, ms[sp]);
-      const float* po = p.ws_o + (head_base + h) * p.max_splits * D + d;
+      const float* po = p.ws_o + row(h) * p.max_splits * D + d;
       float O = 0.0f, Ls = 0.0f;
 #pragma unroll 8
       for (int sp = 0; sp < S; ++sp) {
@@ -222,7 +246,7 @@ struct Finalize {
         O = fmaf(load_coherent(po + static_cast<int64_t>(sp) * D), f, O);
         Ls = fmaf(ls[sp], f, Ls);
       }
-      p.out[(head_base + h) * D + d] = normalise(O, Ls, p.denom_eps);
+      p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
     }
   }
 };

@@ -151,7 +151,10 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 
 // D = 512: 4-wave workgroups at one wave per SIMD (VGPRs + AGPRs for the
 // doubled K buffers and scales).
-template <int D, int G, int NW>
+// kQG: prefill with query groups -- the G column sets are G / p.pq heads x
+// p.pq consecutive queries, each column with its own causal / window limit.
+// Decode and single-query prefill use kQG = false.
+template <int D, int G, int NW, bool kQG>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void sdpa_int4_mfma_kernel(SdpaParams p) {
@@ -171,11 +174,21 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const bool col_used = n < COLS;
   const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
-  const int h0 = kvh * p.gqa + sub * G;
+  // The G column sets are GH heads x pq queries: pq = 1 unless kQG (b is
+  // then the query group of queries b0 .. b_last).
+  const int pq = kQG ? p.pq : 1;
+  const int GH = kQG ? G / pq : G;
+  const int h0 = kvh * p.gqa + sub * GH;
+  const int b0 = b * pq;
+  const int b_last = kQG ? min(b0 + pq - 1, p.nq - 1) : b;
 
-  const SplitRange rg = split_range(p, b, split);
+  const SplitRange rg = kQG ? prefill_range(p, b0, b_last, split) : split_range(p, b, split);
   if (split >= rg.S) return;
   const int t_begin = rg.t_begin, t_end = rg.t_end;
+  // this column's causal / window limits (the queries of a group differ)
+  const int pos = p.n + b0 + (hn / GH);
+  const int col_hi = pos;
+  const int col_lo = p.window > 0 ? pos - p.window + 1 : 0;
 
   using Fin = Finalize<G, D, NW>;
   __shared__ float arena[Fin::kArena];
@@ -219,11 +232,14 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // issued after it)
   uint32_t qraw[NE];
   const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
-  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
+    // element e of column set v = e / D: query min(b0 + v / GH, b_last),
+    // head h0 + v % GH
     const int e = min(static_cast<int>(threadIdx.x) + k * kNT, G * D - 1);
-    const int64_t byte = (qbase + e) * qsz;
+    const int v = e / D;
+    const int64_t qrow = static_cast<int64_t>(min(b0 + v / GH, b_last)) * p.Hq + h0 + v % GH;
+    const int64_t byte = (qrow * D + (e - v * D)) * qsz;
     qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
     if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
   }
@@ -369,7 +385,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         float part = dot * (ks * sf) + kb * qhat;
         part = group_sum<NG>(part);
         const int t = t0 + 16 * tile + 4 * c + i;
-        sc[4 * tile + i] = (t < t_end && col_used) ? part : -INFINITY;
+        bool keep = t < t_end && col_used;
+        if constexpr (kQG) keep = keep && t <= col_hi && t >= col_lo;
+        sc[4 * tile + i] = keep ? part : -INFINITY;
       }
     }
 
@@ -489,13 +507,20 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       Fin::l(arena, wave)[hn] = vhalf == 0 ? l_sum : 0.0f;
     }
   }
-  Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
+  if constexpr (kQG)
+    Fin::run(p, arena, static_cast<int64_t>(b0) * p.Hq + h0, rg.S, split, b * p.Hq + hy, GH,
+             p.Hq, (b_last - b0 + 1) * GH);
+  else
+    Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
 }
 
 template <int D, int G>
 int launch_dg(const SdpaParams& p, dim3 grid, hipStream_t s) {
   constexpr int NW = D == 512 ? 4 : kMfmaWaves;
-  sdpa_int4_mfma_kernel<D, G, NW><<<grid, NW * 64, 0, s>>>(p);
+  if (p.prefill && p.pq > 1)
+    sdpa_int4_mfma_kernel<D, G, NW, true><<<grid, NW * 64, 0, s>>>(p);
+  else
+    sdpa_int4_mfma_kernel<D, G, NW, false><<<grid, NW * 64, 0, s>>>(p);
   TQ_CHECK_LAUNCH("sdpa_int4_mfma_kernel");
   return TQ_OK;
 }

@@ -281,6 +281,10 @@ def test_prompt_cache_file_round_trip(gpu, tmp_path):
     (32, 4, 512, 48, 300, 0, "bf16"),      # Gemma global layer (heads-as-columns kernel)
     (8, 2, 128, 33, 5, 16, "f32"),
     (4, 4, 256, 1, 90, 0, "f16"),          # a single query = decode
+    (16, 8, 128, 37, 20, 5, "bf16"),       # 4 queries per workgroup, partial last group, window 5
+    (4, 4, 256, 7, 0, 0, "f32"),           # GQA 1: 4 queries per workgroup
+    (8, 4, 512, 9, 30, 0, "bf16"),         # D 512, GQA 2
+    (32, 16, 256, 300, 1200, 256, "bf16"),  # long prefix, window, many groups
 ])
 def test_sdpa_prefill_matches_oracle(gpu, Hq, Hkv, D, S, prior, W, qdt):
     """Multi-query attention with the engine fallback's causal + window mask
