@@ -132,7 +132,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
-                          "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+                          "(the multi-GPU sharding of this path is a design, not built)"}))
         sys.exit(2)
     import torch
     from gemma4metal_amd import turboquant as tq
