@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "libturboquant_hip.so")
 ARCH = os.environ.get("TQ_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["tq_runtime.hip", "tq_quant.hip", "tq_sdpa.hip", "tq_sdpa_mfma.hip", "tq_sdpa_hc.hip",
-               "tq_polar.hip"]
+               "tq_prefill.hip", "tq_polar.hip"]
 CXX_SOURCES = ["turboquant.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}", "-Wall",

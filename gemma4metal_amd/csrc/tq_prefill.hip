@@ -1,0 +1,289 @@
+// Multi-query (prefill) attention over the int4 cache with K/V tiles shared
+// by a workgroup's 64 (query, head) rows -- the engine's prefill fallback
+// (engine/gemma4_multilayer.cpp:343-364: dequantize, then masked
+// scaled_dot_product_attention), for head_dim 128 / 256.
+//
+// A workgroup takes all gqa heads of one kv head for 64 / gqa consecutive
+// queries (16 rows per wave) and streams the union of their key ranges in
+// tiles of 32 keys.  Each tile is dequantized once into LDS:
+//   K as fp16 hi / lo rows [key][dim], V transposed as bf16 hi / lo [dim][key]
+// (value = s * nibble + b in fp32, split into a rounded high part and the
+// rounded remainder).
+// Per tile and wave, on the matrix cores (l = lane, m = l % 16, c = l / 16):
+//   S^T = K q^T   v_mfma_f32_16x16x32_f16, A = 16 keys x 32 dims of K, B =
+//                 32 dims x 16 rows of q (hi / lo in registers); the three
+//                 products hi*hi + hi*lo + lo*hi keep ~22 bits.  Lane l then
+//                 holds scores of keys 16 tile + 4c + i for row m.
+//   O^T += V^T P^T  v_mfma_f32_16x16x32_bf16, A = 16 dims x 32 keys of V^T,
+//                 B = the bf16 hi / lo split of the weights: key slot j of
+//                 lane group c is key 16 (j / 4) + 4c + j % 4 -- exactly the
+//                 scores lane l already holds, so no exchange is needed.  Lane
+//                 l accumulates dims 16 blk + 4c + i of row m.
+// The online softmax state (max, denominator) of row m lives in the lanes of
+// column m; each row has its own causal / window limit.
+#include "tq_sdpa_common.h"
+
+namespace tq {
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = 16 * kPfWaves;  // (query, head) rows per workgroup
+constexpr int kPfKeys = 32;             // keys per tile
+
+template <int D>
+struct PfGeom {
+  static constexpr int W = D / 8;                     // packed words per row
+  static constexpr int KSTR = D + 8;                  // K rows in LDS (halves; 16 B pad)
+  static constexpr int VSTR = kPfKeys + 4;            // V^T rows in LDS (halves; 8 B pad)
+  static constexpr int CH = D / 32;                   // K.q k-steps of 32 dims
+  static constexpr int DB = D / 16;                   // 16-dim output blocks
+  static constexpr int KPT = kPfKeys * W / kPfThreads;  // keys per thread in the dequant
+  static_assert(KPT == 2 || KPT == 4, "D");
+};
+
+// Raw int4 words and fp16 scale / bias of this thread's keys of one tile.
+template <int D>
+struct PfRaw {
+  uint32_t kw[PfGeom<D>::KPT], vw[PfGeom<D>::KPT];
+  uint16_t ks[PfGeom<D>::KPT], kb[PfGeom<D>::KPT], vs[PfGeom<D>::KPT], vb[PfGeom<D>::KPT];
+};
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// K and V use different thread roles (word w, keys k0 .. k0 + KPT - 1): K's
+// lanes run along the words of a key (its LDS rows are key-major), V's
+// along the keys of a word (V^T rows are dim-major), so that both LDS
+// stores of a 16-lane phase land in distinct banks.
+template <int D>
+__device__ __forceinline__ void pf_load(PfRaw<D>& R, const SdpaParams& p, int64_t row0, int t0,
+                                        int last, int wk, int kk0, int wv, int kv0) {
+  using Gm = PfGeom<D>;
+#pragma unroll
+  for (int e = 0; e < Gm::KPT; ++e) {
+    const int64_t rk = row0 + min(t0 + kk0 + e, last);
+    const int64_t rv = row0 + min(t0 + kv0 + e, last);
+    R.kw[e] = __builtin_nontemporal_load(p.kq + rk * Gm::W + wk);
+    R.vw[e] = __builtin_nontemporal_load(p.vq + rv * Gm::W + wv);
+    R.ks[e] = static_cast<const uint16_t*>(p.ks)[rk * (D / 64) + (wk >> 3)];
+    R.kb[e] = static_cast<const uint16_t*>(p.kb)[rk * (D / 64) + (wk >> 3)];
+    R.vs[e] = static_cast<const uint16_t*>(p.vs)[rv * (D / 64) + (wv >> 3)];
+    R.vb[e] = static_cast<const uint16_t*>(p.vb)[rv * (D / 64) + (wv >> 3)];
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_int4_kernel(SdpaParams p) {
+  using Gm = PfGeom<D>;
+  constexpr int W = Gm::W, KSTR = Gm::KSTR, VSTR = Gm::VSTR, CH = Gm::CH, DB = Gm::DB;
+  constexpr int KPT = Gm::KPT;
+  __shared__ __attribute__((aligned(16))) _Float16 khi[kPfKeys * KSTR], klo[kPfKeys * KSTR];
+  __shared__ __attribute__((aligned(16))) __bf16 vthi[D * VSTR], vtlo[D * VSTR];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, c = lane >> 4;
+  const int kvh = blockIdx.y;
+  const int gqa = p.gqa;
+  const int qpw = kPfRows / gqa;          // queries per workgroup
+  const int q0 = blockIdx.x * qpw;        // first query of this workgroup
+  const int q_last = min(q0 + qpw, p.nq) - 1;
+  // this lane's row (column m of the wave): query q0 + r / gqa, head r % gqa
+  const int r = 16 * wave + m;
+  const int qo = r / gqa, ho = r - qo * gqa;
+  const bool row_ok = q0 + qo <= q_last;
+  const int qi = min(q0 + qo, q_last);
+  const int pos = p.n + qi;               // absolute position of the query
+  const int W_ = p.window;
+  const int lo = W_ > 0 ? max(0, p.n + q0 + 1 - W_) : 0;  // union of the rows' key ranges
+  const int hi = p.n + q_last + 1;
+  const int last = hi - 1;
+  const int ntile = (hi - lo + kPfKeys - 1) / kPfKeys;
+  const int64_t row0 = static_cast<int64_t>(kvh) * p.cap;
+  const int64_t qrow = static_cast<int64_t>(qi) * p.Hq + kvh * gqa + ho;
+
+  // ---- q of this lane's row: dims 32 ch + 8c .. +7, fp16 hi / lo ----------
+  v8h qh[CH], ql[CH];
+#pragma unroll
+  for (int ch = 0; ch < CH; ++ch) {
+    float f[8];
+    const int64_t e0 = qrow * D + 32 * ch + 8 * c;
+    if (p.q_dtype == TQ_F32) {
+      const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + e0);
+      const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + e0 + 4);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+      const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + e0);
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t a = wd[i] & 0xFFFFu, b = wd[i] >> 16;
+        f[2 * i] = p.q_dtype == TQ_F16 ? h2f(a) : __uint_as_float(static_cast<uint32_t>(a) << 16);
+        f[2 * i + 1] = p.q_dtype == TQ_F16 ? h2f(b) : __uint_as_float(static_cast<uint32_t>(b) << 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = f[i] * p.scale_log2;
+      const _Float16 h = static_cast<_Float16>(x);
+      qh[ch][i] = h;
+      ql[ch][i] = static_cast<_Float16>(x - static_cast<float>(h));
+    }
+  }
+
+  // dequant roles: word w of keys kb0 .. kb0 + KPT - 1 of a tile (K), word
+  // wv of keys kv0 .. (V)
+  constexpr int KB = kPfKeys / KPT;  // key blocks per tile
+  const int w = threadIdx.x % W, kb0 = (threadIdx.x / W) * KPT;
+  const int wv = threadIdx.x / KB, kv0 = (threadIdx.x % KB) * KPT;
+  // raw words of two tiles in flight (tiles it + 1 and it + 2 load while
+  // tile it is computed)
+  PfRaw<D> rawA, rawB;
+  pf_load<D>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
+  pf_load<D>(rawB, p, row0, min(lo + kPfKeys, last), last, w, kb0, wv, kv0);
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  v4f o[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b) o[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto tile = [&](PfRaw<D>& raw, int it) {
+    const int t0 = lo + it * kPfKeys;
+    __syncthreads();  // every wave is done with the previous tile's LDS
+    // ---- dequantize this thread's K / V words into LDS ----------------------
+#pragma unroll
+    for (int e = 0; e < KPT; ++e) {
+      const int key = kb0 + e;
+      const float ks = h2f(raw.ks[e]), kbias = h2f(raw.kb[e]);
+      v8h kh, kl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = fmaf(ks, static_cast<float>((raw.kw[e] >> (4 * j)) & 15u), kbias);
+        const _Float16 h = static_cast<_Float16>(x);
+        kh[j] = h;
+        kl[j] = static_cast<_Float16>(x - static_cast<float>(h));
+      }
+      *reinterpret_cast<v8h*>(&khi[key * KSTR + 8 * w]) = kh;
+      *reinterpret_cast<v8h*>(&klo[key * KSTR + 8 * w]) = kl;
+    }
+    // V^T: the KPT keys of one dim are adjacent -- one 4 / 8 B store each
+    typedef __bf16 vkpt __attribute__((ext_vector_type(KPT)));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      vkpt vh, vl;
+#pragma unroll
+      for (int e = 0; e < KPT; ++e) {
+        const float x = fmaf(h2f(raw.vs[e]), static_cast<float>((raw.vw[e] >> (4 * j)) & 15u),
+                             h2f(raw.vb[e]));
+        const __bf16 h = static_cast<__bf16>(x);
+        vh[e] = h;
+        vl[e] = static_cast<__bf16>(x - static_cast<float>(h));
+      }
+      *reinterpret_cast<vkpt*>(&vthi[(8 * wv + j) * VSTR + kv0]) = vh;
+      *reinterpret_cast<vkpt*>(&vtlo[(8 * wv + j) * VSTR + kv0]) = vl;
+    }
+    __syncthreads();
+    // the words of tile it + 2 go into this buffer while tiles it, it + 1 run
+    pf_load<D>(raw, p, row0, min(t0 + 2 * kPfKeys, last), last, w, kb0, wv, kv0);
+
+    // ---- S^T = K q^T: two 16-key halves -----------------------------------
+    float sc[8];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        const int off = (16 * half + m) * KSTR + 32 * ch + 8 * c;
+        const v8h ah = *reinterpret_cast<const v8h*>(&khi[off]);
+        const v8h al = *reinterpret_cast<const v8h*>(&klo[off]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[ch], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ch], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[ch], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 16 * half + 4 * c + i;
+        const bool keep = row_ok && t <= last && t <= pos && (W_ == 0 || pos - t < W_);
+        sc[4 * half + i] = keep ? acc[i] : -INFINITY;
+      }
+    }
+
+    // ---- online softmax (log2 domain) for row m --------------------------
+    float mt = sc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    if (__any(m_new > m_run)) {
+      const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
+      l_run *= f;
+#pragma unroll
+      for (int b = 0; b < DB; ++b) o[b] *= f;
+      m_run = m_new;
+    }
+    __bf16 ph[8], pl[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float pw = sc[j] == -INFINITY ? 0.0f : fast_exp2(sc[j] - m_run);
+      l_run += pw;
+      ph[j] = static_cast<__bf16>(pw);
+      pl[j] = static_cast<__bf16>(pw - static_cast<float>(ph[j]));
+    }
+    const v8bf bh = v8bf{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
+    const v8bf bl = v8bf{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
+
+    // ---- O^T += V^T P^T ------------------------------------------------------
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+      const int off = (16 * b + m) * VSTR + 4 * c;
+      const u32x2 h0 = *reinterpret_cast<const u32x2*>(&vthi[off]);
+      const u32x2 h1 = *reinterpret_cast<const u32x2*>(&vthi[off + 16]);
+      const u32x2 l0 = *reinterpret_cast<const u32x2*>(&vtlo[off]);
+      const u32x2 l1 = *reinterpret_cast<const u32x2*>(&vtlo[off + 16]);
+      const v8bf ah = __builtin_bit_cast(v8bf, u32x4{h0.x, h0.y, h1.x, h1.y});
+      const v8bf al = __builtin_bit_cast(v8bf, u32x4{l0.x, l0.y, l1.x, l1.y});
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[b], 0, 0, 0);
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[b], 0, 0, 0);
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[b], 0, 0, 0);
+    }
+  };
+  for (int it = 0; it < ntile; it += 2) {
+    tile(rawA, it);
+    if (it + 1 < ntile) tile(rawB, it + 1);
+  }
+
+  // ---- normalise and store row m: dims 16 b + 4c + i -------------------------
+  float l_sum = l_run + shfl_xor_f(l_run, 16);
+  l_sum += shfl_xor_f(l_sum, 32);
+  if (row_ok) {
+    float* out = p.out + qrow * D;
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[16 * b + 4 * c + i] = normalise(o[b][i], l_sum, 0.0f);
+  }
+}
+
+}  // namespace
+
+// Returns -1 when the tile kernel does not serve the shape (the caller then
+// runs the split-K decode kernels in prefill mode).
+int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t s) {
+  if (sb_dtype != TQ_F16 || (D != 128 && D != 256)) return -1;
+  if (p.gqa < 1 || p.gqa > kPfRows || kPfRows % p.gqa != 0) return -1;
+  const int qpw = kPfRows / p.gqa;
+  dim3 grid((p.nq + qpw - 1) / qpw, p.Hkv);
+  if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);
+  else prefill_int4_kernel<256><<<grid, kPfThreads, 0, s>>>(p);
+  TQ_CHECK_LAUNCH("prefill_int4_kernel");
+  return TQ_OK;
+}
+
+}  // namespace tq

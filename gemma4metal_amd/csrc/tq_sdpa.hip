@@ -468,6 +468,14 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
 
   dim3 grid(max_splits, Hkv * n_sub, (batch + pq - 1) / pq);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // A prefill of many queries runs the tile kernel (each K/V tile serves 64
+  // rows); short ones, and shapes it does not serve, the decode kernels.
+  // TQ_PREFILL_IMPL=splitk forces the latter.
+  const char* pimpl = std::getenv("TQ_PREFILL_IMPL");
+  if (prefill && batch >= 64 && !(pimpl && std::string(pimpl) == "splitk")) {
+    const int r = launch_prefill_tiles(p, D, sb_dtype, s);
+    if (r >= 0) return r;
+  }
   if (hc) {
     // 8 heads x 512 dims of partials per split: merged by a separate,
     // parallel kernel rather than one workgroup per kv head

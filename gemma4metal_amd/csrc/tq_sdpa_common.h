@@ -277,6 +277,10 @@ int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
 // D = 512, 8 query heads per workgroup (heads as matrix-core columns), fp16
 // scale/bias: tq_sdpa_hc.hip.
 int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t stream);
+// Prefill with K/V tiles shared by 64 (query, head) rows (tq_prefill.hip);
+// -1 when the shape is not served (D other than 128 / 256, fp32 scales,
+// gqa not dividing 64).
+int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t stream);
 // Merge of the split partials of a launch with ext_merge = 1 (batch b of
 // grid.y): tq_sdpa_hc.hip.
 int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t stream);

@@ -296,3 +296,33 @@ def test_sdpa_prefill_matches_oracle(gpu, Hq, Hkv, D, S, prior, W, qdt):
     out = gpu.sdpa_int4_prefill(qd, *[dev(a) for a in c], prior, Hq // Hkv, 1.0, W)
     ref = O.sdpa_int4_prefill(qv, *c, prior, Hq // Hkv, 1.0, W)
     assert_close(host(out), ref, f"prefill S{S} prior{prior} W{W} D{D}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,prior,W,qdt", [
+    (32, 16, 256, 200, 0, 0, "bf16"),      # GQA 2: 32 queries x 2 heads per workgroup
+    (32, 16, 256, 128, 900, 256, "bf16"),  # cached prefix + window
+    (16, 2, 128, 70, 33, 0, "f16"),        # GQA 8: 8 queries x 8 heads, partial last group
+    (8, 8, 128, 65, 10, 16, "f32"),        # GQA 1: 64 queries per workgroup, tiny window
+    (4, 1, 256, 96, 2000, 0, "bf16"),      # GQA 4, long prefix
+])
+def test_sdpa_prefill_tile_kernel(gpu, Hq, Hkv, D, S, prior, W, qdt):
+    """Prefills of >= 64 queries at D 128 / 256 run the K/V-tile kernel
+    (fp16 / bf16 hi-lo matrix-core products)."""
+    rng = np.random.default_rng(S * 7 + prior + Hq)
+    cap = prior + S + 3
+    qd, qv = queries(rng, (S, Hq, D), qdt)
+    c = host_cache(rng, Hkv, cap, D, "f16")
+    out = gpu.sdpa_int4_prefill(qd, *[dev(a) for a in c], prior, Hq // Hkv, 1.0, W)
+    ref = O.sdpa_int4_prefill(qv, *c, prior, Hq // Hkv, 1.0, W)
+    assert_close(host(out), ref, f"tiles S{S} prior{prior} W{W} D{D} gqa{Hq // Hkv}")
+
+
+def test_sdpa_prefill_tile_and_split_paths_agree(gpu, monkeypatch):
+    rng = np.random.default_rng(91)
+    Hq, Hkv, D, S, prior, W = 32, 16, 256, 160, 500, 300
+    qd, _ = queries(rng, (S, Hq, D), "bf16")
+    cd = [dev(a) for a in host_cache(rng, Hkv, prior + S, D, "f16")]
+    tiles = host(gpu.sdpa_int4_prefill(qd, *cd, prior, 2, 1.0, W))
+    monkeypatch.setenv("TQ_PREFILL_IMPL", "splitk")
+    split = host(gpu.sdpa_int4_prefill(qd, *cd, prior, 2, 1.0, W))
+    assert np.abs(tiles - split).max() < 1e-3
