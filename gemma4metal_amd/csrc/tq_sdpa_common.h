@@ -147,6 +147,14 @@ __device__ __forceinline__ float merge_factor(float m, float M) {
   return m == -INFINITY ? 0.0f : fast_exp2(m - M);
 }
 
+// Lazy online-softmax rescale: a kernel's running max m moves (and its
+// accumulators are rescaled) only when a new score exceeds m by more than
+// this many log2 units, so every weight 2^(s - m) stays <= 2^kLazyMax.
+// Every partial (O, l) is still exact relative to its own m, so the merges
+// are unchanged; the rescale, a read-multiply-write of every accumulator,
+// then runs about once per wave instead of whenever the max grows.
+constexpr float kLazyMax = 8.0f;
+
 // LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G], later
 // reused for the per-split (m, l) of the last workgroup.  NW = waves per
 // workgroup.

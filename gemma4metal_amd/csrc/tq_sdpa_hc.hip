@@ -9,12 +9,15 @@
 // 4 workgroups that each unpack the same K/V.  Here one workgroup takes all
 // 8 heads of a kv head, so every K/V byte is unpacked once:
 //
-// K . q  -- per quant group g (64 dims): v_mfma_i32_16x16x64_i8 with A = 16
-//   keys x 64 nibbles of group g and B = q of the 8 heads (columns 0-7,
-//   repeated in 8-15) as three signed base-256 digits of round(q * 2^F), so
-//   C[key][head] is the exact integer dot of group g.  The score is
-//   sum_g s_g * 2^-F * dot_g + b_g * sum(q over g), taken in every lane of
-//   column (head) and (head + 8).
+// K . q  -- per pair of quant groups (2P, 2P + 1): v_mfma_i32_16x16x64_i8
+//   with A = 16 keys x (32 nibbles of group 2P | 32 of group 2P + 1) and a
+//   block-diagonal B: columns 0-7 the q of the 8 heads over group 2P's dims,
+//   columns 8-15 over group 2P + 1's, zero elsewhere; two such products
+//   (dims 0-31, 32-63 of each group) accumulate into one C.  q is three
+//   signed base-256 digits of round(q * 2^F), so C[key][column] is the exact
+//   integer dot of one group.  A lane adds s_g * 2^-F * dot_g + b_g *
+//   sum(q over g) for its column's group; one cross-lane add (column n and
+//   n ^ 8) then gives the score of head n % 8 in both columns.
 // P . V  -- v_mfma_f32_16x16x32_bf16 per block of 16 V words (2 quant
 //   groups): A = (128 + nibble) as bf16 of 16 words x 32 keys (v_perm_b32 +
 //   and-or), B = the bf16 hi / lo split of p * s_v in columns (head, group of
@@ -49,7 +52,7 @@ constexpr int kHcNG = 8;   // quant groups per row
 constexpr int kHcRB = 256; // bytes per packed row
 
 struct HcBuf {
-  uint32_t kw[2][16];  // [tile][2 g + e]: word 8 g + 2c + e of key 16 tile + m
+  uint32_t kw[2][16];  // [tile][4 P + 2 h + e]: word 8 (2P + c/2) + 4h + 2 (c%2) + e of key 16 tile + m
   uint32_t vw[8][4];   // [slot][blk]: word 16 blk + m of the slot's key
   uint32_t sc[2][4];   // scales of array c for keys 2m, 2m+1 (8 fp16 each)
 };
@@ -63,12 +66,14 @@ __device__ __forceinline__ void hc_load(HcBuf& B, const char* kq, const char* vq
   const char* sb = sc + static_cast<int64_t>(t0) * 16;
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
-    const uint32_t off = static_cast<uint32_t>(min(16 * tile + m, lim)) * kHcRB + c * 8;
+    // lane group c takes group 2P + c / 2 of each pair, dims 16 (c % 2) ..
+    // + 15 of each 32-dim half
+    const uint32_t off = static_cast<uint32_t>(min(16 * tile + m, lim)) * kHcRB + 32 * (c >> 1) + 8 * (c & 1);
 #pragma unroll
-    for (int g = 0; g < kHcNG; ++g) {
-      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(kb + off + 32 * g));
-      B.kw[tile][2 * g] = u.x;
-      B.kw[tile][2 * g + 1] = u.y;
+    for (int j = 0; j < 8; ++j) {  // j = 2 P + h
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(kb + off + 16 * j + 32 * (j >> 1)));
+      B.kw[tile][2 * j] = u.x;
+      B.kw[tile][2 * j + 1] = u.y;
     }
   }
 #pragma unroll
@@ -110,7 +115,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
 
   using Fin = Finalize<G, D, NW>;
   __shared__ float arena[Fin::kArena];
-  __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][group][lane]
+  __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][2 pair + half][lane]
   __shared__ uint32_t sc_lds[NW][4][NG][16];    // [wave][array][group][key pair] fp16 x 2
   __shared__ float red_max[NE][NW];
   __shared__ float sh_qhat[G][NG];
@@ -177,6 +182,11 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
       for (int k = 0; k < NE; ++k) red_max[k][wave] = mx[k];
     }
   }
+  {
+    // the off-diagonal blocks of the B images stay zero
+    uint4* z = &bq_lds[0][0][0];
+    for (int i = threadIdx.x; i < 3 * NG * 64; i += kNT) z[i] = uint4{0u, 0u, 0u, 0u};
+  }
   __syncthreads();
   if (threadIdx.x < G) {
     const int h = threadIdx.x;
@@ -197,23 +207,22 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     const int h = k / KPH;
     const int d = (wave * 64 + k * kNT - h * D) + lane;
     X[k] = static_cast<int>(__builtin_rintf(qv[k] * ldexpf(1.0f, sh_F[h])));
-    // k-slot of dim d in the A operand of group g = d / 64: lane group
-    // cc = (d % 64) / 16, vector element v = 2 ((d % 16) / 8) + d % 2, byte
-    // (d % 8) / 2 -- the order in which the unpack spreads a word's nibbles
-    const int g = d >> 6, r = d & 63, cc = r >> 4, rr = r & 15;
+    // k-slot of dim d (group g = d / 64) in the product of pair g / 2 and
+    // half hf = (d % 64) / 32: lane group cc = (d % 32) / 16 + 2 (g % 2),
+    // column h + 8 (g % 2); vector element v = 2 ((d % 16) / 8) + d % 2,
+    // byte (d % 8) / 2 -- the order in which the unpack spreads a word's
+    // nibbles
+    const int g = d >> 6, r = d & 63, hf = r >> 5, cc = ((r >> 4) & 1) + 2 * (g & 1), rr = r & 15;
     const int s = 4 * (2 * (rr >> 3) + (rr & 1)) + ((rr & 7) >> 1);
     const int d0 = static_cast<int8_t>(X[k] & 0xFF);
     const int X1 = (X[k] - d0) >> 8;
     const int d1 = static_cast<int8_t>(X1 & 0xFF);
     const int d2 = (X1 - d1) >> 8;
-#pragma unroll
-    for (int dup = 0; dup < 2; ++dup) {
-      const int ln = 16 * cc + h + 8 * dup;
-      const int o = ((g * 64) + ln) * 16 + s;
-      bq_bytes[o] = static_cast<uint8_t>(d0);
-      bq_bytes[o + NG * 64 * 16] = static_cast<uint8_t>(d1);
-      bq_bytes[o + 2 * NG * 64 * 16] = static_cast<uint8_t>(d2);
-    }
+    const int ln = 16 * cc + h + 8 * (g & 1);
+    const int o = (((g >> 1) * 2 + hf) * 64 + ln) * 16 + s;
+    bq_bytes[o] = static_cast<uint8_t>(d0);
+    bq_bytes[o + NG * 64 * 16] = static_cast<uint8_t>(d1);
+    bq_bytes[o + 2 * NG * 64 * 16] = static_cast<uint8_t>(d2);
   }
   // per (head, quant group) sums of the fixed-point q, exact: 64 * 2^22 < 2^31
 #pragma unroll
@@ -229,9 +238,10 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   }
   __syncthreads();
   const float sf = ldexpf(1.0f, -sh_F[hh]);
-  float qh[NG];
+  // q sums of this lane's column: head hh, group 2P + m / 8 of pair P
+  float qh[NG / 2];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) qh[g] = sh_qhat[hh][g];
+  for (int P = 0; P < NG / 2; ++P) qh[P] = sh_qhat[hh][2 * P + (m >> 3)];
 
   // ---- main loop ----------------------------------------------------------
   float m_run = -INFINITY, l_run = 0.0f;
@@ -259,38 +269,56 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // K . q per quant group, both 16-key tiles
+    // K . q per pair of quant groups, both 16-key tiles: this lane sums its
+    // column's groups (2P + m / 8)
     float sc[2][4];
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc[tile][i] = 0.0f;
+    auto bop = [&](int dg, int j) {
+      const uint4 u = bq_lds[dg][j][lane];
+      return v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z), static_cast<int>(u.w)};
+    };
+    auto aop = [&](uint32_t w0, uint32_t w1) {
+      return v4i{static_cast<int>(w0 & 0x0F0F0F0Fu), static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
+                 static_cast<int>(w1 & 0x0F0F0F0Fu), static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+    };
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      const uint4 u0 = bq_lds[0][g][lane], u1 = bq_lds[1][g][lane], u2 = bq_lds[2][g][lane];
-      const v4i b0 = v4i{static_cast<int>(u0.x), static_cast<int>(u0.y), static_cast<int>(u0.z), static_cast<int>(u0.w)};
-      const v4i b1 = v4i{static_cast<int>(u1.x), static_cast<int>(u1.y), static_cast<int>(u1.z), static_cast<int>(u1.w)};
-      const v4i b2 = v4i{static_cast<int>(u2.x), static_cast<int>(u2.y), static_cast<int>(u2.z), static_cast<int>(u2.w)};
+    for (int P = 0; P < NG / 2; ++P) {
+      const v4i b00 = bop(0, 2 * P), b01 = bop(0, 2 * P + 1);
+      const v4i b10 = bop(1, 2 * P), b11 = bop(1, 2 * P + 1);
+      const v4i b20 = bop(2, 2 * P), b21 = bop(2, 2 * P + 1);
+      const int gl = 2 * P + (m >> 3);
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile) {
-        const uint32_t w0 = B.kw[tile][2 * g], w1 = B.kw[tile][2 * g + 1];
-        const v4i a = v4i{static_cast<int>(w0 & 0x0F0F0F0Fu), static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
-                          static_cast<int>(w1 & 0x0F0F0F0Fu), static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
-        const v4i acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b0, zero4, 0, 0, 0);
-        const v4i acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b1, zero4, 0, 0, 0);
-        const v4i acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b2, zero4, 0, 0, 0);
-        const uint2 ks = *reinterpret_cast<const uint2*>(&sc_lds[wv][0][g][8 * tile + 2 * c]);
-        const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[wv][1][g][8 * tile + 2 * c]);
+        const v4i a0 = aop(B.kw[tile][4 * P], B.kw[tile][4 * P + 1]);
+        const v4i a1 = aop(B.kw[tile][4 * P + 2], B.kw[tile][4 * P + 3]);
+        v4i acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b00, zero4, 0, 0, 0);
+        v4i acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b10, zero4, 0, 0, 0);
+        v4i acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b20, zero4, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b01, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b11, acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b21, acc2, 0, 0, 0);
+        const uint2 ks = *reinterpret_cast<const uint2*>(&sc_lds[wv][0][gl][8 * tile + 2 * c]);
+        const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[wv][1][gl][8 * tile + 2 * c]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
           const int lo01 = acc0[i] + (acc1[i] << 8);
           const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc2[i]);
           const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
-          sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[g], sc[tile][i]));
+          sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
         }
       }
     }
+    // column n holds the even groups of head n % 8 for n < 8, the odd ones
+    // for n >= 8: add lane m ^ 8 of the same 16-lane row (DPP row rotate 8)
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sc[tile][i] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false));
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
@@ -303,7 +331,9 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     mt = fmaxf(mt, shfl_xor_f(mt, 16));
     mt = fmaxf(mt, shfl_xor_f(mt, 32));
     const float m_new = fmaxf(m_run, mt);
-    if (__any(m_new > m_run)) {
+    if (t0 == base0) {
+      m_run = m_new;  // first batch: nothing accumulated yet
+    } else if (__any(m_new > m_run + kLazyMax)) {
       const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
       l_run *= f;
 #pragma unroll

@@ -199,6 +199,63 @@ def test_sdpa_large_value_range(gpu, Hq, Hkv, D):
     assert np.linalg.norm(d) / np.linalg.norm(ref) <= 1e-3
 
 
+def ramp_inputs(rng, Hq, Hkv, S, cap, D, qdt, sign):
+    """K rows sign * r_t * u + small noise, u a unit direction per kv head and
+    r_t = slope * t; queries along u (norm sqrt(D)).  A query's scores then
+    rise (sign 1) or fall (sign -1) by ~0.1 log2 units per key, so the online
+    softmax's running max moves past any threshold again and again along a
+    wave's keys (or never moves after its first keys)."""
+    slope = 0.1 / np.log2(np.e) / np.sqrt(D)
+    u = rng.standard_normal((Hkv, 1, D))
+    u /= np.linalg.norm(u, axis=-1, keepdims=True)
+    t = np.arange(cap, dtype=np.float64)[None, :, None]
+    k = (sign * slope * t * u + 0.05 * rng.standard_normal((Hkv, cap, D))).astype(np.float32)
+    v = rng.standard_normal((Hkv, cap, D)).astype(np.float32)
+    cache = O.quantize_int4(k, "f16") + O.quantize_int4(v, "f16")
+    g = Hq // Hkv
+    q = np.repeat(u[:, 0, :], g, axis=0) * np.sqrt(D) + 0.1 * rng.standard_normal((S, Hq, D))
+    q = q.astype(np.float32)
+    if qdt == "bf16":
+        bits = O.f32_to_bf16_bits(q)
+        qd = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+        q = O.bf16_bits_to_f32(bits)
+    else:
+        qd = torch.from_numpy(q).cuda()
+    return qd, q, cache
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,L", [
+    (32, 16, 256, 3000),  # matrix-core kernel, D 256
+    (8, 2, 128, 2000),    # matrix-core kernel, D 128
+    (32, 4, 512, 3000),   # heads-as-columns kernel (D 512, GQA 8)
+    (8, 4, 512, 1500),    # matrix-core kernel, D 512 GQA 2
+])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_sdpa_rising_and_falling_scores(gpu, Hq, Hkv, D, L, sign):
+    """Scores that climb (or fall) steadily along the context exercise the
+    online softmax's rescale on every batch of keys (or on none after the
+    first)."""
+    rng = np.random.default_rng(D + L + int(sign > 0))
+    qd, qv, c = ramp_inputs(rng, Hq, Hkv, 1, L, D, "bf16", sign)
+    qd, qv = qd[0], qv[0]
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv)
+    ref = O.sdpa_int4(qv, *c, Hq // Hkv)
+    assert_close(host(out), ref, f"ramp {sign:+.0f} Hq{Hq} Hkv{Hkv} D{D} L{L}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,S,prior", [
+    (32, 16, 256, 128, 900),  # tile kernel
+    (32, 4, 512, 40, 500),    # split-K prefill on the heads-as-columns kernel
+])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_sdpa_prefill_rising_and_falling_scores(gpu, Hq, Hkv, D, S, prior, sign):
+    rng = np.random.default_rng(D + S + int(sign > 0))
+    qd, qv, c = ramp_inputs(rng, Hq, Hkv, S, prior + S, D, "bf16", sign)
+    out = gpu.sdpa_int4_prefill(qd, *[dev(a) for a in c], prior, Hq // Hkv, 1.0, 0)
+    ref = O.sdpa_int4_prefill(qv, *c, prior, Hq // Hkv, 1.0, 0)
+    assert_close(host(out), ref, f"prefill ramp {sign:+.0f} D{D} S{S}")
+
+
 def test_sdpa_global_layer_full_context(gpu):
     """Gemma global layer at 32k (Hq 32, Hkv 4, D 512): cache built on the GPU
     by the (separately bit-exact) quantize kernel, two kv heads checked
