@@ -1,7 +1,7 @@
 // Multi-query (prefill) attention over the int4 cache with K/V tiles shared
 // by a workgroup's 64 (query, head) rows -- the engine's prefill fallback
 // (engine/gemma4_multilayer.cpp:343-364: dequantize, then masked
-// scaled_dot_product_attention), for head_dim 128 / 256.
+// scaled_dot_product_attention), for head_dim 128 / 256 / 512.
 //
 // A workgroup takes all gqa heads of one kv head for 64 / gqa consecutive
 // queries (16 rows per wave) and streams the union of their key ranges in
@@ -41,11 +41,12 @@ template <int D>
 struct PfGeom {
   static constexpr int W = D / 8;                     // packed words per row
   static constexpr int KSTR = D + 8;                  // K rows in LDS (halves; 16 B pad)
-  static constexpr int VSTR = kPfKeys + 4;            // V^T rows in LDS (halves; 8 B pad)
+  static constexpr int KPT = kPfKeys * W / kPfThreads;  // keys per thread in the dequant
+  // V^T rows in LDS (halves): KPT-key stores stay aligned, rows padded
+  static constexpr int VSTR = KPT == 8 ? kPfKeys + 8 : kPfKeys + 4;
   static constexpr int CH = D / 32;                   // K.q k-steps of 32 dims
   static constexpr int DB = D / 16;                   // 16-dim output blocks
-  static constexpr int KPT = kPfKeys * W / kPfThreads;  // keys per thread in the dequant
-  static_assert(KPT == 2 || KPT == 4, "D");
+  static_assert(KPT == 2 || KPT == 4 || KPT == 8, "D");
 };
 
 // Raw int4 words and fp16 scale / bias of this thread's keys of one tile.
@@ -78,8 +79,11 @@ __device__ __forceinline__ void pf_load(PfRaw<D>& R, const SdpaParams& p, int64_
   }
 }
 
+// D = 512: one wave per SIMD (q hi / lo and the O^T accumulators take 256
+// registers), 145 KB of LDS
 template <int D>
-__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kPfThreads)
+__attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void prefill_int4_kernel(SdpaParams p) {
   using Gm = PfGeom<D>;
   constexpr int W = Gm::W, KSTR = Gm::KSTR, VSTR = Gm::VSTR, CH = Gm::CH, DB = Gm::DB;
@@ -142,11 +146,12 @@ void prefill_int4_kernel(SdpaParams p) {
   constexpr int KB = kPfKeys / KPT;  // key blocks per tile
   const int w = threadIdx.x % W, kb0 = (threadIdx.x / W) * KPT;
   const int wv = threadIdx.x / KB, kv0 = (threadIdx.x % KB) * KPT;
-  // raw words of two tiles in flight (tiles it + 1 and it + 2 load while
-  // tile it is computed)
+  // raw words of the tiles in flight: two (tiles it + 1 and it + 2 load
+  // while tile it is computed), one at D = 512 (registers)
+  constexpr int NB = D == 512 ? 1 : 2;
   PfRaw<D> rawA, rawB;
   pf_load<D>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
-  pf_load<D>(rawB, p, row0, min(lo + kPfKeys, last), last, w, kb0, wv, kv0);
+  if constexpr (NB == 2) pf_load<D>(rawB, p, row0, min(lo + kPfKeys, last), last, w, kb0, wv, kv0);
 
   float m_run = -INFINITY, l_run = 0.0f;
   v4f o[DB];
@@ -189,8 +194,8 @@ void prefill_int4_kernel(SdpaParams p) {
       *reinterpret_cast<vkpt*>(&vtlo[(8 * wv + j) * VSTR + kv0]) = vl;
     }
     __syncthreads();
-    // the words of tile it + 2 go into this buffer while tiles it, it + 1 run
-    pf_load<D>(raw, p, row0, min(t0 + 2 * kPfKeys, last), last, w, kb0, wv, kv0);
+    // the words of tile it + NB go into this buffer while tiles it .. run
+    pf_load<D>(raw, p, row0, min(t0 + NB * kPfKeys, last), last, w, kb0, wv, kv0);
 
     // ---- S^T = K q^T: two 16-key halves -----------------------------------
     float sc[8];
@@ -254,9 +259,13 @@ void prefill_int4_kernel(SdpaParams p) {
       o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[b], 0, 0, 0);
     }
   };
-  for (int it = 0; it < ntile; it += 2) {
-    tile(rawA, it);
-    if (it + 1 < ntile) tile(rawB, it + 1);
+  if constexpr (NB == 2) {
+    for (int it = 0; it < ntile; it += 2) {
+      tile(rawA, it);
+      if (it + 1 < ntile) tile(rawB, it + 1);
+    }
+  } else {
+    for (int it = 0; it < ntile; ++it) tile(rawA, it);
   }
 
   // ---- normalise and store row m: dims 16 b + 4c + i -------------------------
@@ -276,12 +285,13 @@ void prefill_int4_kernel(SdpaParams p) {
 // Returns -1 when the tile kernel does not serve the shape (the caller then
 // runs the split-K decode kernels in prefill mode).
 int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t s) {
-  if (sb_dtype != TQ_F16 || (D != 128 && D != 256)) return -1;
+  if (sb_dtype != TQ_F16 || (D != 128 && D != 256 && D != 512)) return -1;
   if (p.gqa < 1 || p.gqa > kPfRows || kPfRows % p.gqa != 0) return -1;
   const int qpw = kPfRows / p.gqa;
   dim3 grid((p.nq + qpw - 1) / qpw, p.Hkv);
   if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);
-  else prefill_int4_kernel<256><<<grid, kPfThreads, 0, s>>>(p);
+  else if (D == 256) prefill_int4_kernel<256><<<grid, kPfThreads, 0, s>>>(p);
+  else prefill_int4_kernel<512><<<grid, kPfThreads, 0, s>>>(p);
   TQ_CHECK_LAUNCH("prefill_int4_kernel");
   return TQ_OK;
 }

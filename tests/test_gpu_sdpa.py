@@ -245,6 +245,7 @@ def test_sdpa_rising_and_falling_scores(gpu, Hq, Hkv, D, L, sign):
 
 @pytest.mark.parametrize("Hq,Hkv,D,S,prior", [
     (32, 16, 256, 128, 900),  # tile kernel
+    (32, 4, 512, 96, 700),    # tile kernel, D 512
     (32, 4, 512, 40, 500),    # split-K prefill on the heads-as-columns kernel
 ])
 @pytest.mark.parametrize("sign", [1.0, -1.0])
@@ -361,9 +362,12 @@ def test_sdpa_prefill_matches_oracle(gpu, Hq, Hkv, D, S, prior, W, qdt):
     (16, 2, 128, 70, 33, 0, "f16"),        # GQA 8: 8 queries x 8 heads, partial last group
     (8, 8, 128, 65, 10, 16, "f32"),        # GQA 1: 64 queries per workgroup, tiny window
     (4, 1, 256, 96, 2000, 0, "bf16"),      # GQA 4, long prefix
+    (32, 4, 512, 100, 300, 0, "bf16"),     # Gemma global layer: 8 queries x 8 heads
+    (8, 1, 512, 70, 40, 64, "f16"),        # D 512 with a window, partial last group
+    (16, 8, 512, 64, 10, 0, "f32"),        # D 512 GQA 2: 32 queries x 2 heads
 ])
 def test_sdpa_prefill_tile_kernel(gpu, Hq, Hkv, D, S, prior, W, qdt):
-    """Prefills of >= 64 queries at D 128 / 256 run the K/V-tile kernel
+    """Prefills of >= 64 queries at D 128 / 256 / 512 run the K/V-tile kernel
     (fp16 / bf16 hi-lo matrix-core products)."""
     rng = np.random.default_rng(S * 7 + prior + Hq)
     cap = prior + S + 3
