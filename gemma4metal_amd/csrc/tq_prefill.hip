@@ -226,7 +226,9 @@ void prefill_int4_kernel(SdpaParams p) {
     mt = fmaxf(mt, shfl_xor_f(mt, 16));
     mt = fmaxf(mt, shfl_xor_f(mt, 32));
     const float m_new = fmaxf(m_run, mt);
-    if (__any(m_new > m_run)) {
+    if (it == 0) {
+      m_run = m_new;  // first tile: nothing accumulated yet
+    } else if (__any(m_new > m_run + kLazyMax)) {
       const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
       l_run *= f;
 #pragma unroll

@@ -398,7 +398,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     mt = fmaxf(mt, shfl_xor_f(mt, 16));
     mt = fmaxf(mt, shfl_xor_f(mt, 32));
     const float m_new = fmaxf(m_run, mt);
-    if (__any(m_new > m_run)) {
+    if (t0 == base0) {
+      m_run = m_new;  // first batch: nothing accumulated yet
+    } else if (__any(m_new > m_run + kLazyMax)) {
       const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
       l_run *= f;
       wsum *= f;
