@@ -7,7 +7,7 @@
 //    u8 per angle, lib/turboquant.cpp:105-109) or packed (u32 + 3 u8 per
 //    block, lib/turboquant.metal:501-600), one fp16 radius per block, and
 //    caller-supplied codebooks;
-//  * the 7-level layout of BASELINE configs[4] ("polar7"): one 128-value block
+//  * the 7-level layout ("polar7"): one 128-value block
 //    per vector -- 64 level-1 angles (4 bits) and 63 angles of levels 2-7
 //    (2 bits) in 12 words, the fp16 radius and the fp16 norm of the QJL
 //    residual in one word, and the 128 sign bits of the QJL residual sketch
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void polar16_sdpa_kernel(SdpaParams p, Attn16 
 }
 
 // ============================================================================
-// configs[4] layout: 7 levels over one 128-value block + QJL
+// polar7 layout: 7 levels over one 128-value block + QJL
 // ============================================================================
 
 struct P7EncParams {
@@ -922,7 +922,7 @@ __device__ __forceinline__ void quarter_sum(float s[G]) {
   }
 }
 
-// Scores only (the compressed_score of configs[4]): four lanes per key, 64
+// Scores only (compressed_score over polar7 keys): four lanes per key, 64
 // keys per pass of a 256-thread workgroup, 1024 keys per workgroup; the next
 // pass's words are loaded while the current pass is scored.  Grid (key
 // blocks, kv heads * head subgroups).
@@ -982,7 +982,7 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 // slot 32 kb + 8 c + j (lane group c of the B operand holds slots 8c .. 8c+7).
 __device__ __forceinline__ int p7_slot(int t) { return (t & 32) | ((t & 3) << 3) | ((t >> 2) & 7); }
 
-// configs[4] attention: polar7 + QJL scores, softmax, int4 V (group 64,
+// polar7 attention: polar7 + QJL scores, softmax, int4 V (group 64,
 // scale/bias SB), split-K.  Per 64-key tile of a wave:
 //  - scores: four lanes per key (quarter qt = lane & 3) over four sub-tiles
 //    of 16 keys; the key words are loaded one tile ahead, the V words of a

@@ -1,5 +1,6 @@
 """Python mirror of the reference's PolarQuant API (``lib/turboquant.h:52-165``)
-and the 7-level PolarQuant + QJL codec of BASELINE configs[4].
+and the 7-level PolarQuant + QJL key codec ("polar7": D = 128, level-1
+angles 4-bit, levels 2-7 2-bit, a 128-bit QJL residual sketch).
 
 Every computation runs in ``libturboquant_hip.so`` (C ABI in
 ``include/tq_c_api.h``); torch only holds device memory and the stream.
@@ -234,7 +235,7 @@ def cos_sin_table(cb: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# 7-level PolarQuant + QJL over D = 128
+# polar7: 7-level PolarQuant + QJL over D = 128
 # ---------------------------------------------------------------------------
 
 def polar7_codebooks(device=None):
@@ -248,7 +249,7 @@ def polar7_codebooks(device=None):
 
 
 class Polar7Codec:
-    """Keys of one model layer in the configs[4] layout: a D x D orthogonal
+    """Keys of one model layer in the polar7 layout: a D x D orthogonal
     preconditioner P, an m x D QJL sketch matrix S, the codebooks.
 
     Caches are ``angles`` (Hkv, cap, 12) u32, ``norms`` (Hkv, cap) u32 (fp16

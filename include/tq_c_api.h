@@ -254,7 +254,7 @@ int tq_compressed_sdpa(const float* q, int num_heads, const uint8_t* idx_l1, con
                        int num_kv_heads, int n_keys, int dim, int block_size, float scale,
                        float* out, void* workspace, size_t workspace_bytes, void* stream);
 
-/* ---- 7-level PolarQuant + QJL (D = 128) ----------------
+/* ---- 7-level PolarQuant + QJL ("polar7"; D = 128) ---------------------------
  * No reference kernel: the same polar recursion as polar_quantize over one
  * 128-value block (7 levels; level-1 angles 4-bit, levels 2-7 2-bit) plus
  * the QJL residual sketch the reference README describes (README.md:11,176).

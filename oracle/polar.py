@@ -1,5 +1,6 @@
 """NumPy restatement of the reference's PolarQuant kernels, and of the QJL
-residual sketch and compressed-key decode attention of BASELINE configs[4].
+residual sketch and compressed-key decode attention of the 7-level "polar7"
+layout (D = 128).
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
@@ -13,7 +14,7 @@ Reference locations restated:
   by the index of the nearest codebook entry under the linear distance
   |theta - c|, first minimum wins (``:38-42``); the last radius is stored as
   fp16 (``:96``).  The reference hard-codes 16-value blocks (4 levels); the
-  same recursion over one 128-value block (7 levels) is the configs[4]
+  same recursion over one 128-value block (7 levels) is the polar7
   encoding.
 * preconditioning -- ``y = x P^T`` before encoding (``lib/turboquant.cpp:102``),
   ``x = y P`` after decoding (``:122``).
@@ -273,7 +274,7 @@ def compressed_sdpa(q, i1, i2, i3, i4, radii, cbs, values, scale, gqa=1, block=1
 
 
 # --------------------------------------------------------------------------
-# 7-level full-vector PolarQuant + QJL (D = 128)
+# polar7: 7-level full-vector PolarQuant + QJL (D = 128)
 # --------------------------------------------------------------------------
 
 P7_D = 128
@@ -345,7 +346,7 @@ def sketch_f32(S, r):
 
 
 def polar7_encode(x, P, S, cb1=None, cb2=None):
-    """configs[4] key encoding of x (N, 128) float32.
+    """polar7 key encoding of x (N, 128) float32.
 
     Returns (angles u32 (N, 12), norms f16 (N, 2) = (radius, ||r||),
     qjl u32 (N, 4) with bit i of word i/32 = [(S r)_i >= 0]).
@@ -392,7 +393,7 @@ def qjl_signs(qjl):
 
 
 def polar7_scores(qp, qs, angles, norms, qjl, gqa, scale=1.0, cb1=None, cb2=None):
-    """configs[4] scores, float64: scores[h, n] = scale * (<q'_h, yhat_n> +
+    """polar7 scores, float64: scores[h, n] = scale * (<q'_h, yhat_n> +
     sqrt(pi/2)/m * ||r_n|| * <qs_h, sign_n>) for keys of kv head h // gqa.
 
     qp (Hq, 128) = P q (the rotated query), qs (Hq, 128) = S qp;
@@ -415,7 +416,7 @@ def polar7_scores(qp, qs, angles, norms, qjl, gqa, scale=1.0, cb1=None, cb2=None
 
 def polar7_sdpa_int4v(qp, qs, angles, norms, qjl, vq, vs, vb, gqa, scale=1.0,
                       window=0, kv_len=None, cb1=None, cb2=None):
-    """configs[4] attention: softmax over the polar+QJL scores of the attended
+    """polar7 attention: softmax over the polar+QJL scores of the attended
     keys, times the int4-dequantized V; empty key set -> 0.  Keys/values of
     rows [0, kv_len) with the sdpa_int4 window rule."""
     from oracle import oracle as O
@@ -441,12 +442,12 @@ def qjl_query(qp, S):
 
 
 def polar7_row_bytes(D: int = P7_D, sb_bytes: int = 2) -> int:
-    """Bytes per (kv head, token) of configs[4]: K = 48 B angles + 16 B sketch
+    """Bytes per (kv head, token) of the polar7 layout: K = 48 B angles + 16 B sketch
     + 4 B (radius, ||r||) fp16; V = int4 nibbles + fp16 scale/bias."""
     return P7_WORDS * 4 + QJL_M // 8 + 4 + D // 2 + 2 * (D // 64) * sb_bytes
 
 
 def polar7_decode_bytes(Hq: int, Hkv: int, attended: int, q_bytes: int = 4) -> int:
-    """Algorithmic bytes of one configs[4] decode layer: the compressed K and
+    """Algorithmic bytes of one polar7 decode layer: the compressed K and
     int4 V rows once, q' and S q' (fp32) in, fp32 out."""
     return Hkv * attended * polar7_row_bytes() + 2 * Hq * P7_D * q_bytes + Hq * P7_D * 4

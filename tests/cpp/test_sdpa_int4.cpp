@@ -79,7 +79,7 @@ int main() {
   fails += run_case(16, 16, 10, 256, 0, gen);      // the reference test's shape
   fails += run_case(32, 16, 786, 256, 1024, gen);  // sliding layer
   fails += run_case(32, 4, 300, 512, 0, gen);      // global layer
-  fails += run_case(2, 1, 33, 128, 0, gen);
+  fails += run_case(2, 1, 33, 128, 0, gen);        // tiny decode (the reference test shape)
   fails += run_case(32, 16, 3000, 256, 1024, gen); // window active
   return fails == 0 ? 0 : 1;
 }

@@ -42,7 +42,7 @@ def make():
     wq, s, b = O.quantize_int4(x, "f16", mode="minmax")
     out["quant_minmax_f16"] = dict(x=x, wq=wq, scales=s, biases=b)
 
-    # Hq 2, Hkv 1, D 128, L 33, RMS-normed q/k, scale 1
+    # tiny decode: Hq 2, Hkv 1, D 128, L 33, RMS-normed q/k, scale 1
     rng = np.random.default_rng(20260)
     q = O.rms_norm(rng.standard_normal((2, 128)).astype(f32))
     k = O.rms_norm(rng.standard_normal((1, 33, 128)).astype(f32))
@@ -63,7 +63,7 @@ def make():
     out["polar16"] = dict(x=xv, P=P, cb1=cbs[0], cb2=cbs[1], cb3=cbs[2], cb4=cbs[3],
                           i1=i1, i2=i2, i3=i3, i4=i4, radii=rad, p1=p1, p2=p2, p3=p3, p4=p4)
 
-    # configs[4] layout: 7 levels + QJL, and scores of 2 query heads
+    # polar7 layout: 7 levels + QJL, and scores of 2 query heads
     rng = np.random.default_rng(47)
     xk = rng.standard_normal((2, 30, 128)).astype(f32)
     P = np.linalg.qr(rng.standard_normal((128, 128)))[0].astype(f32)

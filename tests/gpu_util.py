@@ -1,5 +1,5 @@
 """Shared helpers for the GPU parity tests: seeded inputs, host<->device moves
-and the BASELINE tolerance (2e-3 max-abs, 1e-3 relative, fp32 accumulation)."""
+and the parity tolerance (2e-3 max-abs, 1e-3 relative, fp32 accumulation)."""
 import numpy as np
 import torch
 

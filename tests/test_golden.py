@@ -73,7 +73,7 @@ def test_gpu_matches_sdpa_fixture(gpu):
     from tests.gpu_util import assert_close, dev, host
     g = load("sdpa_tiny")
     out = gpu.sdpa_int4(dev(g["q"]), *[dev(g[k]) for k in ("kq", "ks", "kb", "vq", "vs", "vb")], 2, 1.0, 0)
-    assert_close(host(out), g["out"], "golden configs[0]")
+    assert_close(host(out), g["out"], "golden tiny decode")
 
 
 @pytest.mark.gpu

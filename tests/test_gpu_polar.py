@@ -2,7 +2,7 @@
 
 Encoders (indices, packed words, fp16 radii/norms, sketch bits): bit-exact.
 Decoders: 1e-5 relative to the vector norm.  Scores: max-abs 1e-3.
-Attention: the BASELINE tolerance (2e-3 abs / 1e-3 rel)."""
+Attention: the parity tolerance (2e-3 abs / 1e-3 rel)."""
 import numpy as np
 import pytest
 import torch
@@ -269,7 +269,7 @@ def test_polar7_sdpa_empty_and_prefix(pq):
 
 
 def test_polar7_full_size_two_heads(pq):
-    """BASELINE configs[4] size (Hq 32, Hkv 16, L 32768): the whole launch,
+    """The polar7 decode shape (Hq 32, Hkv 16, L 32768): the whole launch,
     checked against the oracle on two kv heads' outputs."""
     Hq, Hkv, L = 32, 16, 32768
     rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 2026, Hkv, L)

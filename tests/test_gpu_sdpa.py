@@ -16,10 +16,10 @@ def host_cache(rng, Hkv, cap, D, sb="f16"):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,L,W,qdt,sb,scale", [
-    (2, 1, 128, 33, 0, "f32", "f32", 1.0),        # BASELINE config 1 (tiny)
+    (2, 1, 128, 33, 0, "f32", "f32", 1.0),        # tiny decode (the reference test shape)
     (2, 1, 128, 33, 0, "f32", "f16", 1.0),
     (16, 16, 256, 10, 0, "f32", "f32", 1.0),      # reference test shape
-    (32, 16, 256, 786, 1024, "bf16", "f16", 1.0), # BASELINE config 2 layer
+    (32, 16, 256, 786, 1024, "bf16", "f16", 1.0), # Gemma sliding layer at L 786
     (32, 16, 256, 1500, 1024, "bf16", "f16", 1.0),  # window active
     (32, 4, 512, 300, 0, "bf16", "f16", 1.0),     # Gemma global layer (GQA 8, D 512)
     (8, 1, 512, 129, 0, "f16", "f32", 0.0625),
@@ -62,7 +62,7 @@ def test_sdpa_empty_keys_zero(gpu):
 
 
 def test_sdpa_full_context_split_k(gpu):
-    """BASELINE config 3 at its largest size (L=262144): cache built on the GPU
+    """The context sweep's largest size (L=262144): cache built on the GPU
     by the (separately bit-exact) quantize kernel, checked against the C oracle
     on the heads of two kv heads."""
     from oracle import coracle

@@ -41,7 +41,7 @@ def torch_reference(q, cache, gqa, scale, window, n):
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,L,W,scale", [
-    (2, 1, 128, 33, 0, 1.0),        # BASELINE config 1 shape
+    (2, 1, 128, 33, 0, 1.0),        # tiny decode shape
     (16, 16, 256, 10, 0, 1.0),      # reference test shape (tests/test_sdpa_int4.cpp:13)
     (32, 16, 256, 300, 128, 1.0),   # sliding layer, window active
     (8, 1, 512, 77, 0, 0.125),      # global-layer-like GQA 8, D 512
