@@ -156,11 +156,11 @@ __device__ __forceinline__ float merge_factor(float m, float M) {
 constexpr float kLazyMax = 8.0f;
 
 // LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G], later
-// reused for the per-split (m, l) of the last workgroup.  NW = waves per
-// workgroup.
-template <int G, int D, int NW = kWaves>
+// reused for the per-split (m, l) of the last workgroup.  NW = partial
+// results per workgroup (one per wave, or per key stream), NT = threads.
+template <int G, int D, int NW = kWaves, int NT = NW * 64>
 struct Finalize {
-  static constexpr int kNT = NW * 64;
+  static constexpr int kNT = NT;
   static constexpr int kArena = (NW * G * D + 2 * NW * G) > (2 * G * kMaxSplits)
                                     ? (NW * G * D + 2 * NW * G)
                                     : (2 * G * kMaxSplits);

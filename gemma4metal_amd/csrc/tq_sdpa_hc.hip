@@ -58,11 +58,11 @@ struct HcBuf {
 };
 
 // Loads of the 32 keys at t0 (rows clamped to `last`, the uniform limit
-// `lim` = last - t0 >= 0), non-temporal, uniform base + 32-bit lane offset.
-__device__ __forceinline__ void hc_load(HcBuf& B, const char* kq, const char* vq, const char* sc,
-                                        int t0, int lim, int m, int c) {
+// `lim` = last - t0 >= 0), non-temporal, uniform base + 32-bit lane offset:
+// K words and the scale arrays, and the V words, as separate parts.
+__device__ __forceinline__ void hc_load_k(uint32_t (&kw)[2][16], uint32_t (&scw)[2][4], const char* kq,
+                                          const char* sc, int t0, int lim, int m, int c) {
   const char* kb = kq + static_cast<int64_t>(t0) * kHcRB;
-  const char* vb = vq + static_cast<int64_t>(t0) * kHcRB;
   const char* sb = sc + static_cast<int64_t>(t0) * 16;
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
@@ -72,100 +72,55 @@ __device__ __forceinline__ void hc_load(HcBuf& B, const char* kq, const char* vq
 #pragma unroll
     for (int j = 0; j < 8; ++j) {  // j = 2 P + h
       const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(kb + off + 16 * j + 32 * (j >> 1)));
-      B.kw[tile][2 * j] = u.x;
-      B.kw[tile][2 * j + 1] = u.y;
+      kw[tile][2 * j] = u.x;
+      kw[tile][2 * j + 1] = u.y;
     }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t off = static_cast<uint32_t>(min(16 * (j >> 2) + 4 * c + (j & 3), lim)) * kHcRB + m * 4;
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
-      B.vw[j][blk] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb + off + 64 * blk));
   }
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const uint32_t off = static_cast<uint32_t>(min(2 * m + e, lim)) * 16;
     const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sb + off));
-    B.sc[e][0] = u.x; B.sc[e][1] = u.y; B.sc[e][2] = u.z; B.sc[e][3] = u.w;
+    scw[e][0] = u.x; scw[e][1] = u.y; scw[e][2] = u.z; scw[e][3] = u.w;
   }
+}
+
+__device__ __forceinline__ void hc_load_v(uint32_t (&vw)[8][4], const char* vq, int t0, int lim, int m,
+                                          int c) {
+  const char* vb = vq + static_cast<int64_t>(t0) * kHcRB;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t off = static_cast<uint32_t>(min(16 * (j >> 2) + 4 * c + (j & 3), lim)) * kHcRB + m * 4;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+      vw[j][blk] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb + off + 64 * blk));
+  }
+}
+
+__device__ __forceinline__ void hc_load(HcBuf& B, const char* kq, const char* vq, const char* sc,
+                                        int t0, int lim, int m, int c) {
+  hc_load_k(B.kw, B.sc, kq, sc, t0, lim, m, c);
+  hc_load_v(B.vw, vq, t0, lim, m, c);
 }
 
 __device__ __forceinline__ float hc_half(uint32_t w, int hi) {
   return __half2float(__ushort_as_half(static_cast<uint16_t>(hi ? (w >> 16) : (w & 0xFFFFu))));
 }
 
-__global__ __launch_bounds__(kHcWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void sdpa_int4_hc_kernel(SdpaParams p) {
-  constexpr int NW = kHcWaves, D = kHcD, G = kHcG, NG = kHcNG;
-  constexpr int kNT = NW * 64;
-  constexpr int kIter = 32 * NW;          // keys per workgroup iteration
-  constexpr int NE = G * D / kNT;         // q elements per thread
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int m = lane & 15, c = lane >> 4;
-  const int hh = m & 7;                   // this lane's head (column m)
-  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
-  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
-  const int h0 = kvh * p.gqa + sub * G;
-
-  const SplitRange rg = split_range(p, b, split);
-  if (split >= rg.S) return;
-  const int t_end = rg.t_end;
-
-  using Fin = Finalize<G, D, NW>;
-  __shared__ float arena[Fin::kArena];
-  __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][2 pair + half][lane]
-  __shared__ uint32_t sc_lds[NW][4][NG][16];    // [wave][array][group][key pair] fp16 x 2
-  __shared__ float red_max[NE][NW];
-  __shared__ float sh_qhat[G][NG];
-  __shared__ int sh_F[G];
-
-  const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
-  const char* kq_rows = reinterpret_cast<const char*>(p.kq + row0 * (D / 8));
-  const char* vq_rows = reinterpret_cast<const char*>(p.vq + row0 * (D / 8));
-  // lane group c loads scale array c: k scale, k bias, v scale, v bias
-  const void* sc_base = c == 0 ? p.ks : (c == 1 ? p.kb : (c == 2 ? p.vs : p.vb));
-  const char* sc_rows = static_cast<const char*>(sc_base) + row0 * 16;
-
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const int base0 = rg.t_begin + wv * 32;
-  const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
-  const int last = t_end - 1;
-  const int safe_last = max(last, 0);
-
-  // q first (one dword per element, no branch around the load), then the
-  // first iteration's K/V, which stay in flight through the prologue
-  uint32_t qraw[NE];
-  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
-  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
-    qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-    if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  HcBuf bufA, bufB;
-  {
-    const int t0 = min(base0, safe_last);
-    hc_load(bufA, kq_rows, vq_rows, sc_rows, t0, safe_last - t0, m, c);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- prologue: q of the 8 heads as 22-bit fixed point, B images in LDS --
-  float qv[NE];
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const uint32_t w = qraw[k];
-    const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
-                    : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
-                                          : __uint_as_float(w << 16);
-    qv[k] = f * p.scale_log2;
-  }
+// Prologue of both kernels: the scaled q of the 8 heads (qv[k] = element
+// threadIdx.x + kNT k of the 8 x 512 block) as 22-bit fixed point, scattered
+// into the block-diagonal B images of the K.q products (bq_lds, whose
+// off-diagonal blocks are zeroed here), the per-(head, group) sums of the
+// fixed-point q (sh_qhat) and the per-head exponent F (sh_F).  NW = waves of
+// the workgroup.  Ends with a barrier.
+template <int kNT, int NW>
+__device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT], uint4 (&bq_lds)[3][kHcNG][64],
+                                           float (&red_max)[kHcG * kHcD / kNT][NW],
+                                           float (&sh_qhat)[kHcG][kHcNG], int (&sh_F)[kHcG], int lane,
+                                           int wave) {
+  constexpr int D = kHcD, G = kHcG, NG = kHcNG, NE = G * D / kNT;
+  static_assert(D % kNT == 0, "slot -> head");
   // slot (k, w) = elements 64 w + kNT k + lane: one quant group of head
   // (kNT k) / D (kNT divides D, so k alone names the head)
-  static_assert(D % kNT == 0, "slot -> head");
   constexpr int KPH = D / kNT;  // slots k per head
   // the NE wave reductions step through the shuffle offsets together, so
   // their LDS round trips overlap
@@ -237,6 +192,77 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     }
   }
   __syncthreads();
+}
+
+__global__ __launch_bounds__(kHcWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void sdpa_int4_hc_kernel(SdpaParams p) {
+  constexpr int NW = kHcWaves, D = kHcD, G = kHcG, NG = kHcNG;
+  constexpr int kNT = NW * 64;
+  constexpr int kIter = 32 * NW;          // keys per workgroup iteration
+  constexpr int NE = G * D / kNT;         // q elements per thread
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, c = lane >> 4;
+  const int hh = m & 7;                   // this lane's head (column m)
+  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+
+  const SplitRange rg = split_range(p, b, split);
+  if (split >= rg.S) return;
+  const int t_end = rg.t_end;
+
+  using Fin = Finalize<G, D, NW>;
+  __shared__ float arena[Fin::kArena];
+  __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][2 pair + half][lane]
+  __shared__ uint32_t sc_lds[NW][4][NG][16];    // [wave][array][group][key pair] fp16 x 2
+  __shared__ float red_max[NE][NW];
+  __shared__ float sh_qhat[G][NG];
+  __shared__ int sh_F[G];
+
+  const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
+  const char* kq_rows = reinterpret_cast<const char*>(p.kq + row0 * (D / 8));
+  const char* vq_rows = reinterpret_cast<const char*>(p.vq + row0 * (D / 8));
+  // lane group c loads scale array c: k scale, k bias, v scale, v bias
+  const void* sc_base = c == 0 ? p.ks : (c == 1 ? p.kb : (c == 2 ? p.vs : p.vb));
+  const char* sc_rows = static_cast<const char*>(sc_base) + row0 * 16;
+
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int base0 = rg.t_begin + wv * 32;
+  const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
+  const int last = t_end - 1;
+  const int safe_last = max(last, 0);
+
+  // q first (one dword per element, no branch around the load), then the
+  // first iteration's K/V, which stay in flight through the prologue
+  uint32_t qraw[NE];
+  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
+    qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
+    if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  HcBuf bufA, bufB;
+  {
+    const int t0 = min(base0, safe_last);
+    hc_load(bufA, kq_rows, vq_rows, sc_rows, t0, safe_last - t0, m, c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- prologue: q of the 8 heads as 22-bit fixed point, B images in LDS --
+  float qv[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const uint32_t w = qraw[k];
+    const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
+                    : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
+                                          : __uint_as_float(w << 16);
+    qv[k] = f * p.scale_log2;
+  }
+  hc_q_image<kNT, NW>(qv, bq_lds, red_max, sh_qhat, sh_F, lane, wave);
   const float sf = ldexpf(1.0f, -sh_F[hh]);
   // q sums of this lane's column: head hh, group 2P + m / 8 of pair P
   float qh[NG / 2];
@@ -442,6 +468,349 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
 }
 
+// ---- wave-specialised variant ---------------------------------------------
+// The kernel above runs one wave per SIMD: every wave does both products of
+// its keys, and at 1,500 instructions per 32 keys with nothing to hide its
+// stalls, it is bound by issue, not HBM.  Here eight waves (two per SIMD)
+// split the work of four 32-key streams:
+//   producer s (waves 0-3): loads the K words and the four scale arrays of
+//     stream s, computes K . q and the online softmax, and builds the P . V
+//     B operands (bf16 hi / lo of p * s_v per block) plus the offset and bias
+//     sums, staged in LDS (two slots, by iteration parity);
+//   consumer s (waves 4-7): loads the V words of stream s, builds the A
+//     operands and runs the 64 P . V products, one iteration behind.
+// One barrier per step orders a slot's writes before its reads and the
+// reads before its reuse two steps later.  Each role runs as its own code
+// path (no buffer lives across a join of the two), through the same number
+// of barriers: every wave runs the same even number of steps, and blocks
+// past a stream's end are masked.  The accumulators of the consumer (128)
+// and the doubled buffers of either role fit 256 registers, two waves per
+// SIMD.
+constexpr int kHs = 4;  // key streams (producer / consumer pairs)
+
+__global__ __launch_bounds__(2 * kHs * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_int4_hc2_kernel(SdpaParams p) {
+  constexpr int NS = kHs, NWV = 2 * kHs, D = kHcD, G = kHcG, NG = kHcNG;
+  constexpr int kNT = NWV * 64;
+  constexpr int kIter = 32 * NS;   // keys per workgroup iteration
+  constexpr int NE = G * D / kNT;  // q elements per thread
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, c = lane >> 4;
+  const int hh = m & 7;  // this lane's head (column m)
+  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
+  const int h0 = kvh * p.gqa + sub * G;
+
+  const SplitRange rg = split_range(p, b, split);
+  if (split >= rg.S) return;
+  const int t_end = rg.t_end;
+
+  using Fin = Finalize<G, D, NS, kNT>;
+  // the P . V operand slots during the loop, the finalisation arena after it
+  constexpr int kPvWords = 2 * NS * 4 * 2 * 64 * 4;  // [slot][stream][blk][hi/lo][lane] x uint4
+  constexpr int kArenaWords = Fin::kArena > kPvWords ? Fin::kArena : kPvWords;
+  __shared__ __attribute__((aligned(16))) float arena[kArenaWords];
+  uint4* pv_lds = reinterpret_cast<uint4*>(arena);
+  __shared__ uint4 bq_lds[3][NG][64];         // K MFMA B operands [digit][2 pair + half][lane]
+  __shared__ uint32_t sc_lds[NS][4][NG][16];  // [stream][array][group][key pair] fp16 x 2
+  __shared__ float f_lds[2][NS][16];          // rescale factor per column, by slot
+  __shared__ float off_lds[NS][4][16];        // final offset per (block, column)
+  __shared__ float red_max[NE][NWV];
+  __shared__ float sh_qhat[G][NG];
+  __shared__ int sh_F[G];
+
+  const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
+  const char* kq_rows = reinterpret_cast<const char*>(p.kq + row0 * (D / 8));
+  const char* vq_rows = reinterpret_cast<const char*>(p.vq + row0 * (D / 8));
+  const void* sc_base = c == 0 ? p.ks : (c == 1 ? p.kb : (c == 2 ? p.vs : p.vb));
+  const char* sc_rows = static_cast<const char*>(sc_base) + row0 * 16;
+
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const bool producer = wv < NS;
+  const int s = producer ? wv : wv - NS;  // key stream
+  const int base0 = rg.t_begin + s * 32;
+  // steps of every wave: the iterations of stream 0 (the longest), rounded
+  // up to even (the loops below take two per trip)
+  const int nit0 = (t_end - rg.t_begin + kIter - 1) / kIter;
+  const int NI = nit0 + (nit0 & 1);
+  const int last = t_end - 1;
+  const int safe_last = max(last, 0);
+  auto tclamp = [&](int t0) { return min(t0, safe_last); };
+
+  auto load_q = [&](uint32_t (&qraw)[NE]) {
+    const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+    const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
+      qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
+      if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
+    }
+  };
+  auto q_image = [&](const uint32_t (&qraw)[NE]) {
+    float qv[NE];
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      const uint32_t w = qraw[k];
+      const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
+                      : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
+                                            : __uint_as_float(w << 16);
+      qv[k] = f * p.scale_log2;
+    }
+    hc_q_image<kNT, NWV>(qv, bq_lds, red_max, sh_qhat, sh_F, lane, wave);
+  };
+  const v4i zero4 = v4i{0, 0, 0, 0};
+
+  if (producer) {
+    // ======================= producer: K . q, softmax, B operands ===========
+    uint32_t qraw[NE];
+    load_q(qraw);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t kA[2][16], kB[2][16], sA[2][4], sB[2][4];
+    hc_load_k(kA, sA, kq_rows, sc_rows, tclamp(base0), safe_last - tclamp(base0), m, c);
+    __builtin_amdgcn_sched_barrier(0);
+    q_image(qraw);
+    const float sf = ldexpf(1.0f, -sh_F[hh]);
+    float qh[NG / 2];
+#pragma unroll
+    for (int P = 0; P < NG / 2; ++P) qh[P] = sh_qhat[hh][2 * P + (m >> 3)];
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    float wsum[4], bacc[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) wsum[blk] = bacc[blk] = 0.0f;
+
+    auto produce = [&](const uint32_t (&kw)[2][16], const uint32_t (&scw)[2][4], int st) {
+      const int t0 = base0 + st * kIter, slot = st & 1;
+      // scales -> LDS [array][group][key pair]
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const uint32_t a0 = scw[0][g >> 1], a1 = scw[1][g >> 1];
+        sc_lds[s][c][g][m] = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u)) : ((a0 & 0xFFFFu) | (a1 << 16));
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // K . q per pair of quant groups (as in the kernel above)
+      float sc[2][4];
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[tile][i] = 0.0f;
+      auto bop = [&](int dg, int j) {
+        const uint4 u = bq_lds[dg][j][lane];
+        return v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z), static_cast<int>(u.w)};
+      };
+      auto aop = [&](uint32_t w0, uint32_t w1) {
+        return v4i{static_cast<int>(w0 & 0x0F0F0F0Fu), static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
+                   static_cast<int>(w1 & 0x0F0F0F0Fu), static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+      };
+#pragma unroll
+      for (int P = 0; P < NG / 2; ++P) {
+        const v4i b00 = bop(0, 2 * P), b01 = bop(0, 2 * P + 1);
+        const v4i b10 = bop(1, 2 * P), b11 = bop(1, 2 * P + 1);
+        const v4i b20 = bop(2, 2 * P), b21 = bop(2, 2 * P + 1);
+        const int gl = 2 * P + (m >> 3);
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile) {
+          const v4i a0 = aop(kw[tile][4 * P], kw[tile][4 * P + 1]);
+          const v4i a1 = aop(kw[tile][4 * P + 2], kw[tile][4 * P + 3]);
+          v4i acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b00, zero4, 0, 0, 0);
+          v4i acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b10, zero4, 0, 0, 0);
+          v4i acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b20, zero4, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b01, acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b11, acc1, 0, 0, 0);
+          acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b21, acc2, 0, 0, 0);
+          const uint2 ks = *reinterpret_cast<const uint2*>(&sc_lds[s][0][gl][8 * tile + 2 * c]);
+          const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[s][1][gl][8 * tile + 2 * c]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int lo01 = acc0[i] + (acc1[i] << 8);
+            const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc2[i]);
+            const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
+            sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
+          }
+        }
+      }
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[tile][i] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false));
+          if (t0 + 16 * tile + 4 * c + i >= t_end) sc[tile][i] = -INFINITY;
+        }
+
+      // online softmax (lazy rescale); the factor goes to the consumer
+      float mt = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+      mt = fmaxf(mt, shfl_xor_f(mt, 16));
+      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      const float m_new = fmaxf(m_run, mt);
+      float f = 1.0f;
+      if (st == 0) {
+        m_run = m_new;  // first batch: nothing accumulated yet
+      } else if (__any(m_new > m_run + kLazyMax)) {
+        f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
+        l_run *= f;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+          wsum[blk] *= f;
+          bacc[blk] *= f;
+        }
+        m_run = m_new;
+      }
+      if (c == 0) f_lds[slot][s][m] = f;
+      float pw[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sj = sc[j >> 2][j & 3];
+        pw[j] = sj == -INFINITY ? 0.0f : fast_exp2(sj - m_run);
+        l_run += pw[j];
+      }
+
+      // B operands of the P . V products per block of 16 V words
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const int gv = 2 * blk + (m >> 3);
+        const uint2 vs0 = *reinterpret_cast<const uint2*>(&sc_lds[s][2][gv][2 * c]);
+        const uint2 vs1 = *reinterpret_cast<const uint2*>(&sc_lds[s][2][gv][8 + 2 * c]);
+        const uint2 vb0 = *reinterpret_cast<const uint2*>(&sc_lds[s][3][gv][2 * c]);
+        const uint2 vb1 = *reinterpret_cast<const uint2*>(&sc_lds[s][3][gv][8 + 2 * c]);
+        const uint32_t vsw[4] = {vs0.x, vs0.y, vs1.x, vs1.y};
+        const uint32_t vbw[4] = {vb0.x, vb0.y, vb1.x, vb1.y};
+        __bf16 hi[8], lo[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float w = pw[j] * hc_half(vsw[j >> 1], j & 1);
+          hi[j] = static_cast<__bf16>(w);
+          const float hf = static_cast<float>(hi[j]);
+          lo[j] = static_cast<__bf16>(w - hf);
+          wsum[blk] += hf + static_cast<float>(lo[j]);
+          bacc[blk] = fmaf(pw[j], hc_half(vbw[j >> 1], j & 1), bacc[blk]);
+        }
+        const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
+        const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+        uint4* dst = pv_lds + (((slot * NS + s) * 4 + blk) * 2) * 64 + lane;
+        dst[0] = __builtin_bit_cast(uint4, bhi);
+        dst[64] = __builtin_bit_cast(uint4, blo);
+      }
+    };
+
+    for (int st = 0; st < NI; st += 2) {
+      hc_load_k(kB, sB, kq_rows, sc_rows, tclamp(base0 + (st + 1) * kIter),
+                safe_last - tclamp(base0 + (st + 1) * kIter), m, c);
+      __builtin_amdgcn_sched_barrier(0);
+      produce(kA, sA, st);
+      __syncthreads();
+      hc_load_k(kA, sA, kq_rows, sc_rows, tclamp(base0 + (st + 2) * kIter),
+                safe_last - tclamp(base0 + (st + 2) * kIter), m, c);
+      __builtin_amdgcn_sched_barrier(0);
+      produce(kB, sB, st + 1);
+      __syncthreads();
+    }
+    __syncthreads();  // the consumers' last step
+
+    // per-column results: (m, l) into the arena (the operand slots are dead
+    // now), the offsets of the weight sums for the consumers
+    float l_sum = l_run + shfl_xor_f(l_run, 16);
+    l_sum += shfl_xor_f(l_sum, 32);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      wsum[blk] += shfl_xor_f(wsum[blk], 16);
+      wsum[blk] += shfl_xor_f(wsum[blk], 32);
+      bacc[blk] += shfl_xor_f(bacc[blk], 16);
+      bacc[blk] += shfl_xor_f(bacc[blk], 32);
+      if (c == 0) off_lds[s][blk][m] = bacc[blk] - 128.0f * wsum[blk];
+    }
+    if (c == 0 && m < 8) {
+      Fin::m(arena, s)[hh] = m_run;
+      Fin::l(arena, s)[hh] = l_sum;
+    }
+    __syncthreads();  // offsets visible to the consumers
+  } else {
+    // ======================= consumer: P . V ================================
+    uint32_t qraw[NE];
+    load_q(qraw);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t vA[8][4], vB[8][4];
+    hc_load_v(vA, vq_rows, tclamp(base0), safe_last - tclamp(base0), m, c);
+    __builtin_amdgcn_sched_barrier(0);
+    q_image(qraw);
+
+    v4f cv[4][8];  // [blk][2 byte + nibble half]
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int ff = 0; ff < 8; ++ff) cv[blk][ff] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t magic = 0x43004300u;  // bf16 of (128 + nibble)
+    asm volatile("" : "+v"(magic));
+
+    auto consume = [&](const uint32_t (&vw)[8][4], int st) {
+      const int slot = st & 1;
+      const float f = f_lds[slot][s][m];
+      if (__any(f != 1.0f)) {
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+          for (int ff = 0; ff < 8; ++ff) cv[blk][ff] *= f;
+      }
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const uint4* src = pv_lds + (((slot * NS + s) * 4 + blk) * 2) * 64 + lane;
+        const v8bf bhi = __builtin_bit_cast(v8bf, src[0]);
+        const v8bf blo = __builtin_bit_cast(v8bf, src[64]);
+#pragma unroll
+        for (int by = 0; by < 4; ++by) {
+          const uint32_t sel = static_cast<uint32_t>(by) | (0x0Cu << 8) |
+                               (static_cast<uint32_t>(4 + by) << 16) | (0x0Cu << 24);
+          uint32_t alo[4], ahi[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t x = __builtin_amdgcn_perm(vw[2 * r + 1][blk], vw[2 * r][blk], sel);
+            alo[r] = (x & 0x000F000Fu) | magic;
+            ahi[r] = ((x >> 4) & 0x000F000Fu) | magic;
+          }
+          const v8bf a_lo = __builtin_bit_cast(v8bf, u32x4{alo[0], alo[1], alo[2], alo[3]});
+          const v8bf a_hi = __builtin_bit_cast(v8bf, u32x4{ahi[0], ahi[1], ahi[2], ahi[3]});
+          cv[blk][2 * by] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, bhi, cv[blk][2 * by], 0, 0, 0);
+          cv[blk][2 * by + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, bhi, cv[blk][2 * by + 1], 0, 0, 0);
+          cv[blk][2 * by] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, blo, cv[blk][2 * by], 0, 0, 0);
+          cv[blk][2 * by + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, blo, cv[blk][2 * by + 1], 0, 0, 0);
+        }
+      }
+    };
+
+    __syncthreads();  // the producers' step 0
+    for (int st = 0; st < NI; st += 2) {
+      hc_load_v(vB, vq_rows, tclamp(base0 + (st + 1) * kIter), safe_last - tclamp(base0 + (st + 1) * kIter), m, c);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(vA, st);
+      __syncthreads();
+      hc_load_v(vA, vq_rows, tclamp(base0 + (st + 2) * kIter), safe_last - tclamp(base0 + (st + 2) * kIter), m, c);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(vB, st + 1);
+      __syncthreads();
+    }
+    __syncthreads();  // the producers' offsets
+    // lane (m, c) holds V words 16 blk + 4c + i of column m; the column's
+    // group in block blk is 2 blk + m / 8, the words' group 2 blk + c / 2
+    if ((c >> 1) == (m >> 3)) {
+      float* o = Fin::o(arena, s, hh);
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const float off = off_lds[s][blk][m];
+#pragma unroll
+        for (int ff = 0; ff < 8; ++ff)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[8 * (16 * blk + 4 * c + i) + ff] = cv[blk][ff][i] + off;
+      }
+    }
+  }
+  Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
+}
+
 // Merge of split partials written with ext_merge = 1: eight outputs (four
 // dims each) per wave, eight lanes per output taking every eighth split,
 // combined with three shuffles.  The partials come from an earlier kernel,
@@ -503,8 +872,18 @@ int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t s) {
 }
 
 int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t s) {
-  sdpa_int4_hc_kernel<<<grid, kHcWaves * 64, 0, s>>>(p);
-  TQ_CHECK_LAUNCH("sdpa_int4_hc_kernel");
+  // TQ_HC_IMPL=1 selects the one-wave-per-SIMD kernel
+  static const bool one = [] {
+    const char* v = std::getenv("TQ_HC_IMPL");
+    return v && v[0] == '1';
+  }();
+  if (one) {
+    sdpa_int4_hc_kernel<<<grid, kHcWaves * 64, 0, s>>>(p);
+    TQ_CHECK_LAUNCH("sdpa_int4_hc_kernel");
+  } else {
+    sdpa_int4_hc2_kernel<<<grid, 2 * kHs * 64, 0, s>>>(p);
+    TQ_CHECK_LAUNCH("sdpa_int4_hc2_kernel");
+  }
   return TQ_OK;
 }
 
