@@ -811,42 +811,68 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
 }
 
-// Merge of split partials written with ext_merge = 1: eight outputs (four
-// dims each) per wave, eight lanes per output taking every eighth split,
-// combined with three shuffles.  The partials come from an earlier kernel,
-// so plain loads see them.  Grid (ceil(Hq * D / 4 / 32), batch).
+// Merge of split partials written with ext_merge = 1.  A wave takes four
+// outputs (four dims each), sixteen lanes per output; a lane takes splits
+// sl, sl + 16, ...: four at a time, each group's (m, l) and O partials
+// loaded together (one memory round trip per 64 splits), folded into the
+// lane's running (m, l, O), then the 16 lanes merge by shuffles.  The
+// partials come from an earlier kernel, so plain loads see them.  Grid
+// (ceil(Hq * D / 4 / 16), batch).
 __global__ __launch_bounds__(256) void merge_splits_kernel(SdpaParams p, int D) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sl = lane & 7;
+  const int sl = lane & 15;
   const int D4 = D / 4;
-  const int o0 = (blockIdx.x * 4 + wave) * 8;  // first output of this wave
+  const int o0 = (blockIdx.x * 4 + wave) * 4;  // first output of this wave
   const int b = blockIdx.y;
-  if (o0 >= p.Hq * D4) return;                 // whole waves (Hq * D4 % 8 == 0)
+  if (o0 >= p.Hq * D4) return;                 // whole waves (Hq * D4 % 4 == 0)
   const SplitRange rg = split_range(p, b, 0);
   const int S = rg.S;
   if (S == 1) return;                          // written by the attention kernel
-  const int o = o0 + (lane >> 3);
+  const int o = o0 + (lane >> 4);
   const int h = o / D4, d4 = o - h * D4;
   const int64_t head = static_cast<int64_t>(b) * p.Hq + h;
   const float* ml = p.ws_ml + head * p.max_splits * 2;
-  float M = -INFINITY;
-  for (int s = sl; s < S; s += 8) M = fmaxf(M, ml[2 * s]);
-  M = fmaxf(M, shfl_xor_f(M, 1));
-  M = fmaxf(M, shfl_xor_f(M, 2));
-  M = fmaxf(M, shfl_xor_f(M, 4));
+  const float* po = p.ws_o + head * p.max_splits * D + 4 * d4;
+  float M = -INFINITY, L = 0.0f;
   float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  float L = 0.0f;
-  for (int s = sl; s < S; s += 8) {
-    const float f = merge_factor(ml[2 * s], M);
-    const float4 v = *reinterpret_cast<const float4*>(p.ws_o + (head * p.max_splits + s) * D + 4 * d4);
-    O.x = fmaf(v.x, f, O.x);
-    O.y = fmaf(v.y, f, O.y);
-    O.z = fmaf(v.z, f, O.z);
-    O.w = fmaf(v.w, f, O.w);
-    L = fmaf(ml[2 * s + 1], f, L);
-  }
+  for (int s0 = 0; s0 < S; s0 += 64) {
+    float mk[4], lk[4];
+    float4 ok[4];
 #pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
+    for (int k = 0; k < 4; ++k) {
+      const int sp = min(s0 + sl + 16 * k, S - 1);  // clamped; dropped below
+      mk[k] = ml[2 * sp];
+      lk[k] = ml[2 * sp + 1];
+      ok[k] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(sp) * D);
+    }
+    float Mn = M;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (s0 + sl + 16 * k >= S) mk[k] = -INFINITY;
+      Mn = fmaxf(Mn, mk[k]);
+    }
+    const float fr = merge_factor(M, Mn);
+    L *= fr;
+    O.x *= fr; O.y *= fr; O.z *= fr; O.w *= fr;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float f = merge_factor(mk[k], Mn);
+      L = fmaf(lk[k], f, L);
+      O.x = fmaf(ok[k].x, f, O.x);
+      O.y = fmaf(ok[k].y, f, O.y);
+      O.z = fmaf(ok[k].z, f, O.z);
+      O.w = fmaf(ok[k].w, f, O.w);
+    }
+    M = Mn;
+  }
+  float Mall = M;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) Mall = fmaxf(Mall, shfl_xor_f(Mall, off));
+  const float f = merge_factor(M, Mall);
+  L *= f;
+  O.x *= f; O.y *= f; O.z *= f; O.w *= f;
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
     O.x += shfl_xor_f(O.x, off);
     O.y += shfl_xor_f(O.y, off);
     O.z += shfl_xor_f(O.z, off);
@@ -866,7 +892,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(SdpaParams p, int D) 
 
 int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t s) {
   const int outs = p.Hq * D / 4;
-  merge_splits_kernel<<<dim3((outs + 31) / 32, batch), 256, 0, s>>>(p, D);
+  merge_splits_kernel<<<dim3((outs + 15) / 16, batch), 256, 0, s>>>(p, D);
   TQ_CHECK_LAUNCH("merge_splits_kernel");
   return TQ_OK;
 }
