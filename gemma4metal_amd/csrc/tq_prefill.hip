@@ -62,6 +62,46 @@ __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_
 // lanes run along the words of a key (its LDS rows are key-major), V's
 // along the keys of a word (V^T rows are dim-major), so that both LDS
 // stores of a 16-lane phase land in distinct banks.
+// Dequantization of one tile's raw words (this thread's keys) into the LDS
+// images: K as fp16 hi / lo rows, V^T as bf16 hi / lo (value s * n + b in
+// fp32, then its rounded high part and the rounded remainder).
+template <int D>
+__device__ __forceinline__ void pf_dequant(const PfRaw<D>& raw, _Float16* khi, _Float16* klo, __bf16* vthi,
+                                           __bf16* vtlo, int w, int kb0, int wv, int kv0) {
+  using Gm = PfGeom<D>;
+  constexpr int KSTR = Gm::KSTR, VSTR = Gm::VSTR, KPT = Gm::KPT;
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) {
+    const int key = kb0 + e;
+    const float ks = h2f(raw.ks[e]), kbias = h2f(raw.kb[e]);
+    v8h kh, kl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = fmaf(ks, static_cast<float>((raw.kw[e] >> (4 * j)) & 15u), kbias);
+      const _Float16 h = static_cast<_Float16>(x);
+      kh[j] = h;
+      kl[j] = static_cast<_Float16>(x - static_cast<float>(h));
+    }
+    *reinterpret_cast<v8h*>(&khi[key * KSTR + 8 * w]) = kh;
+    *reinterpret_cast<v8h*>(&klo[key * KSTR + 8 * w]) = kl;
+  }
+  // V^T: the KPT keys of one dim are adjacent -- one 4 / 8 / 16 B store each
+  typedef __bf16 vkpt __attribute__((ext_vector_type(KPT)));
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    vkpt vh, vl;
+#pragma unroll
+    for (int e = 0; e < KPT; ++e) {
+      const float x = fmaf(h2f(raw.vs[e]), static_cast<float>((raw.vw[e] >> (4 * j)) & 15u), h2f(raw.vb[e]));
+      const __bf16 h = static_cast<__bf16>(x);
+      vh[e] = h;
+      vl[e] = static_cast<__bf16>(x - static_cast<float>(h));
+    }
+    *reinterpret_cast<vkpt*>(&vthi[(8 * wv + j) * VSTR + kv0]) = vh;
+    *reinterpret_cast<vkpt*>(&vtlo[(8 * wv + j) * VSTR + kv0]) = vl;
+  }
+}
+
 template <int D>
 __device__ __forceinline__ void pf_load(PfRaw<D>& R, const SdpaParams& p, int64_t row0, int t0,
                                         int last, int wk, int kk0, int wv, int kv0) {
@@ -162,37 +202,7 @@ void prefill_int4_kernel(SdpaParams p) {
     const int t0 = lo + it * kPfKeys;
     __syncthreads();  // every wave is done with the previous tile's LDS
     // ---- dequantize this thread's K / V words into LDS ----------------------
-#pragma unroll
-    for (int e = 0; e < KPT; ++e) {
-      const int key = kb0 + e;
-      const float ks = h2f(raw.ks[e]), kbias = h2f(raw.kb[e]);
-      v8h kh, kl;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float x = fmaf(ks, static_cast<float>((raw.kw[e] >> (4 * j)) & 15u), kbias);
-        const _Float16 h = static_cast<_Float16>(x);
-        kh[j] = h;
-        kl[j] = static_cast<_Float16>(x - static_cast<float>(h));
-      }
-      *reinterpret_cast<v8h*>(&khi[key * KSTR + 8 * w]) = kh;
-      *reinterpret_cast<v8h*>(&klo[key * KSTR + 8 * w]) = kl;
-    }
-    // V^T: the KPT keys of one dim are adjacent -- one 4 / 8 B store each
-    typedef __bf16 vkpt __attribute__((ext_vector_type(KPT)));
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      vkpt vh, vl;
-#pragma unroll
-      for (int e = 0; e < KPT; ++e) {
-        const float x = fmaf(h2f(raw.vs[e]), static_cast<float>((raw.vw[e] >> (4 * j)) & 15u),
-                             h2f(raw.vb[e]));
-        const __bf16 h = static_cast<__bf16>(x);
-        vh[e] = h;
-        vl[e] = static_cast<__bf16>(x - static_cast<float>(h));
-      }
-      *reinterpret_cast<vkpt*>(&vthi[(8 * wv + j) * VSTR + kv0]) = vh;
-      *reinterpret_cast<vkpt*>(&vtlo[(8 * wv + j) * VSTR + kv0]) = vl;
-    }
+    pf_dequant<D>(raw, khi, klo, vthi, vtlo, w, kb0, wv, kv0);
     __syncthreads();
     // the words of tile it + NB go into this buffer while tiles it .. run
     pf_load<D>(raw, p, row0, min(t0 + NB * kPfKeys, last), last, w, kb0, wv, kv0);
@@ -282,6 +292,191 @@ void prefill_int4_kernel(SdpaParams p) {
   }
 }
 
+// ---- wave-specialised variant (D = 128, 256) ------------------------------
+// The kernel above has every wave dequantize its share of a tile, wait at a
+// barrier, then run its matrix-core products: at one workgroup per CU the
+// two phases never overlap.  Here eight waves (two per SIMD) split them:
+// loader waves 0-3 dequantize tile st + 1 into one of two LDS image slots
+// while compute waves 4-7 run tile st from the other; one barrier per step.
+// Both roles pass the same number of barriers (an even number of steps;
+// a step past the last tile dequantizes clamped rows, whose scores the
+// mask drops).  Two slots take 141 KB at D = 256, so D = 512 keeps the
+// kernel above.
+template <int D>
+__global__ __launch_bounds__(2 * kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_int4_ws_kernel(SdpaParams p) {
+  using Gm = PfGeom<D>;
+  constexpr int W = Gm::W, KSTR = Gm::KSTR, VSTR = Gm::VSTR, CH = Gm::CH, DB = Gm::DB;
+  constexpr int KPT = Gm::KPT;
+  constexpr int KI = kPfKeys * KSTR, VI = D * VSTR;  // halves per K / V^T image
+  __shared__ __attribute__((aligned(16))) _Float16 khi[2][KI], klo[2][KI];
+  __shared__ __attribute__((aligned(16))) __bf16 vthi[2][VI], vtlo[2][VI];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const bool loader = wave < kPfWaves;
+  const int m = lane & 15, c = lane >> 4;
+  const int kvh = blockIdx.y;
+  const int gqa = p.gqa;
+  const int qpw = kPfRows / gqa;          // queries per workgroup
+  const int q0 = blockIdx.x * qpw;        // first query of this workgroup
+  const int q_last = min(q0 + qpw, p.nq) - 1;
+  const int W_ = p.window;
+  const int lo = W_ > 0 ? max(0, p.n + q0 + 1 - W_) : 0;  // union of the rows' key ranges
+  const int hi = p.n + q_last + 1;
+  const int last = hi - 1;
+  const int ntile = (hi - lo + kPfKeys - 1) / kPfKeys;
+  const int nt2 = ntile + (ntile & 1);
+  const int64_t row0 = static_cast<int64_t>(kvh) * p.cap;
+
+  if (loader) {
+    // ================= loaders: raw words -> LDS images ======================
+    const int tid = threadIdx.x;
+    constexpr int KB = kPfKeys / KPT;
+    const int w = tid % W, kb0 = (tid / W) * KPT;
+    const int wv = tid / KB, kv0 = (tid % KB) * KPT;
+    PfRaw<D> rawA, rawB;
+    pf_load<D>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
+    for (int st = 0; st < nt2; st += 2) {
+      pf_load<D>(rawB, p, row0, min(lo + (st + 1) * kPfKeys, last), last, w, kb0, wv, kv0);
+      pf_dequant<D>(rawA, khi[0], klo[0], vthi[0], vtlo[0], w, kb0, wv, kv0);
+      __syncthreads();
+      pf_load<D>(rawA, p, row0, min(lo + (st + 2) * kPfKeys, last), last, w, kb0, wv, kv0);
+      pf_dequant<D>(rawB, khi[1], klo[1], vthi[1], vtlo[1], w, kb0, wv, kv0);
+      __syncthreads();
+    }
+    __syncthreads();  // the compute waves' last tile
+    return;
+  }
+
+  // =================== compute waves: S^T, softmax, O^T ======================
+  // this lane's row (column m of its wave): query q0 + r / gqa, head r % gqa
+  const int r = 16 * (wave - kPfWaves) + m;
+  const int qo = r / gqa, ho = r - qo * gqa;
+  const bool row_ok = q0 + qo <= q_last;
+  const int qi = min(q0 + qo, q_last);
+  const int pos = p.n + qi;               // absolute position of the query
+  const int64_t qrow = static_cast<int64_t>(qi) * p.Hq + kvh * gqa + ho;
+
+  // q of this lane's row: dims 32 ch + 8c .. +7, fp16 hi / lo
+  v8h qh[CH], ql[CH];
+#pragma unroll
+  for (int ch = 0; ch < CH; ++ch) {
+    float f[8];
+    const int64_t e0 = qrow * D + 32 * ch + 8 * c;
+    if (p.q_dtype == TQ_F32) {
+      const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + e0);
+      const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + e0 + 4);
+      f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    } else {
+      const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.q) + e0);
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t a = wd[i] & 0xFFFFu, b = wd[i] >> 16;
+        f[2 * i] = p.q_dtype == TQ_F16 ? h2f(a) : __uint_as_float(static_cast<uint32_t>(a) << 16);
+        f[2 * i + 1] = p.q_dtype == TQ_F16 ? h2f(b) : __uint_as_float(static_cast<uint32_t>(b) << 16);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = f[i] * p.scale_log2;
+      const _Float16 h = static_cast<_Float16>(x);
+      qh[ch][i] = h;
+      ql[ch][i] = static_cast<_Float16>(x - static_cast<float>(h));
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  v4f o[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b) o[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto tile = [&](const _Float16* kh_, const _Float16* kl_, const __bf16* vh_, const __bf16* vl_, int it) {
+    const int t0 = lo + it * kPfKeys;
+    // ---- S^T = K q^T: two 16-key halves -----------------------------------
+    float sc[8];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        const int off = (16 * half + m) * KSTR + 32 * ch + 8 * c;
+        const v8h ah = *reinterpret_cast<const v8h*>(&kh_[off]);
+        const v8h al = *reinterpret_cast<const v8h*>(&kl_[off]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[ch], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ch], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[ch], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 16 * half + 4 * c + i;
+        const bool keep = row_ok && t <= last && t <= pos && (W_ == 0 || pos - t < W_);
+        sc[4 * half + i] = keep ? acc[i] : -INFINITY;
+      }
+    }
+    // ---- online softmax (log2 domain) for row m --------------------------
+    float mt = sc[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
+    mt = fmaxf(mt, shfl_xor_f(mt, 16));
+    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    if (it == 0) {
+      m_run = m_new;  // first tile: nothing accumulated yet
+    } else if (__any(m_new > m_run + kLazyMax)) {
+      const float f = (m_new == m_run) ? 1.0f : merge_factor(m_run, m_new);
+      l_run *= f;
+#pragma unroll
+      for (int b = 0; b < DB; ++b) o[b] *= f;
+      m_run = m_new;
+    }
+    __bf16 ph[8], pl[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float pw = sc[j] == -INFINITY ? 0.0f : fast_exp2(sc[j] - m_run);
+      l_run += pw;
+      ph[j] = static_cast<__bf16>(pw);
+      pl[j] = static_cast<__bf16>(pw - static_cast<float>(ph[j]));
+    }
+    const v8bf bh = v8bf{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
+    const v8bf bl = v8bf{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
+    // ---- O^T += V^T P^T ------------------------------------------------------
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+      const int off = (16 * b + m) * VSTR + 4 * c;
+      const u32x2 h0 = *reinterpret_cast<const u32x2*>(&vh_[off]);
+      const u32x2 h1 = *reinterpret_cast<const u32x2*>(&vh_[off + 16]);
+      const u32x2 l0 = *reinterpret_cast<const u32x2*>(&vl_[off]);
+      const u32x2 l1 = *reinterpret_cast<const u32x2*>(&vl_[off + 16]);
+      const v8bf ah = __builtin_bit_cast(v8bf, u32x4{h0.x, h0.y, h1.x, h1.y});
+      const v8bf al = __builtin_bit_cast(v8bf, u32x4{l0.x, l0.y, l1.x, l1.y});
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[b], 0, 0, 0);
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[b], 0, 0, 0);
+      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[b], 0, 0, 0);
+    }
+  };
+
+  __syncthreads();  // tile 0 is in slot 0
+  for (int st = 0; st < nt2; st += 2) {
+    tile(khi[0], klo[0], vthi[0], vtlo[0], st);
+    __syncthreads();
+    tile(khi[1], klo[1], vthi[1], vtlo[1], st + 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store row m: dims 16 b + 4c + i -------------------------
+  float l_sum = l_run + shfl_xor_f(l_run, 16);
+  l_sum += shfl_xor_f(l_sum, 32);
+  if (row_ok) {
+    float* out = p.out + qrow * D;
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[16 * b + 4 * c + i] = normalise(o[b][i], l_sum, 0.0f);
+  }
+}
+
 }  // namespace
 
 // Returns -1 when the tile kernel does not serve the shape (the caller then
@@ -291,7 +486,14 @@ int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t s
   if (p.gqa < 1 || p.gqa > kPfRows || kPfRows % p.gqa != 0) return -1;
   const int qpw = kPfRows / p.gqa;
   dim3 grid((p.nq + qpw - 1) / qpw, p.Hkv);
-  if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);
+  // TQ_PREFILL_WS=0 selects the one-role kernel at D 128 / 256
+  static const bool ws = [] {
+    const char* v = std::getenv("TQ_PREFILL_WS");
+    return !(v && v[0] == '0');
+  }();
+  if (D == 128 && ws) prefill_int4_ws_kernel<128><<<grid, 2 * kPfThreads, 0, s>>>(p);
+  else if (D == 256 && ws) prefill_int4_ws_kernel<256><<<grid, 2 * kPfThreads, 0, s>>>(p);
+  else if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);
   else if (D == 256) prefill_int4_kernel<256><<<grid, kPfThreads, 0, s>>>(p);
   else prefill_int4_kernel<512><<<grid, kPfThreads, 0, s>>>(p);
   TQ_CHECK_LAUNCH("prefill_int4_kernel");
