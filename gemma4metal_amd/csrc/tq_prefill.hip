@@ -486,11 +486,9 @@ int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t s
   if (p.gqa < 1 || p.gqa > kPfRows || kPfRows % p.gqa != 0) return -1;
   const int qpw = kPfRows / p.gqa;
   dim3 grid((p.nq + qpw - 1) / qpw, p.Hkv);
-  // TQ_PREFILL_WS=0 selects the one-role kernel at D 128 / 256
-  static const bool ws = [] {
-    const char* v = std::getenv("TQ_PREFILL_WS");
-    return !(v && v[0] == '0');
-  }();
+  // TQ_PREFILL_WS=0 selects the one-role kernel at D 128 / 256 (read per call)
+  const char* wsv = std::getenv("TQ_PREFILL_WS");
+  const bool ws = !(wsv && wsv[0] == '0');
   if (D == 128 && ws) prefill_int4_ws_kernel<128><<<grid, 2 * kPfThreads, 0, s>>>(p);
   else if (D == 256 && ws) prefill_int4_ws_kernel<256><<<grid, 2 * kPfThreads, 0, s>>>(p);
   else if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);

@@ -378,6 +378,37 @@ def test_sdpa_prefill_tile_kernel(gpu, Hq, Hkv, D, S, prior, W, qdt):
     assert_close(host(out), ref, f"tiles S{S} prior{prior} W{W} D{D} gqa{Hq // Hkv}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,L,W", [(32, 4, 5000, 0), (32, 4, 3001, 1024), (16, 2, 129, 0)])
+def test_d512_one_wave_and_wave_specialised_kernels_agree(gpu, monkeypatch, Hq, Hkv, L, W):
+    """The two D=512 GQA-8 kernels (TQ_HC_IMPL=1 selects the one-wave one)
+    compute the same products: outputs agree to fp32 rounding."""
+    rng = np.random.default_rng(L + W)
+    qd, qv = queries(rng, (Hq, 512), "bf16")
+    c = host_cache(rng, Hkv, L, 512, "f16")
+    cd = [dev(a) for a in c]
+    two = host(gpu.sdpa_int4(qd, *cd, Hq // Hkv, 1.0, W))
+    monkeypatch.setenv("TQ_HC_IMPL", "1")
+    one = host(gpu.sdpa_int4(qd, *cd, Hq // Hkv, 1.0, W))
+    assert np.abs(two - one).max() < 1e-4
+    assert_close(one, O.sdpa_int4(qv, *c, Hq // Hkv, 1.0, W), "one-wave D512")
+
+
+@pytest.mark.parametrize("D,gqa", [(256, 2), (128, 8)])
+def test_prefill_tile_kernels_agree(gpu, monkeypatch, D, gqa):
+    """The wave-specialised and one-role tile kernels (TQ_PREFILL_WS=0)
+    compute the same products in the same order: bit-identical outputs."""
+    rng = np.random.default_rng(D + gqa)
+    Hkv, S, prior, W = 4, 130, 400, 256
+    qd, qv = queries(rng, (S, Hkv * gqa, D), "bf16")
+    c = host_cache(rng, Hkv, prior + S, D, "f16")
+    cd = [dev(a) for a in c]
+    ws = host(gpu.sdpa_int4_prefill(qd, *cd, prior, gqa, 1.0, W))
+    monkeypatch.setenv("TQ_PREFILL_WS", "0")
+    one = host(gpu.sdpa_int4_prefill(qd, *cd, prior, gqa, 1.0, W))
+    assert np.array_equal(ws, one)
+    assert_close(ws, O.sdpa_int4_prefill(qv, *c, prior, gqa, 1.0, W), f"ws prefill D{D}")
+
+
 def test_sdpa_prefill_tile_and_split_paths_agree(gpu, monkeypatch):
     rng = np.random.default_rng(91)
     Hq, Hkv, D, S, prior, W = 32, 16, 256, 160, 500, 300
