@@ -995,9 +995,13 @@ __device__ __forceinline__ int p7_slot(int t) { return (t & 32) | ((t & 3) << 3)
 //    bf16 keeps fp32's exponent range, so no scale of V can overflow it.
 //    The 128 offset (128 * sum(hi + lo)) and the bias term sum(p * b_v) are
 //    accumulated per column and removed at the end.
-template <int G, typename SB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
-  constexpr int NW = 4, D = 128;
+// Waves per polar7 attention workgroup: eight, two per SIMD at one workgroup
+// per CU, sharing the workgroup's staged query tables.
+constexpr int kP7Waves = 8;
+
+template <int G, typename SB, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
+  constexpr int D = 128;
   __shared__ P7Tables<G> T;
   using Fin = Finalize<G, D, NW>;
   __shared__ float arena[Fin::kArena];
@@ -1683,12 +1687,13 @@ int tq_polar7_sdpa_int4v(const float* q_tables, const uint32_t* angles,
   p.vq = v_quant; p.vs = v_scales; p.vb = v_biases;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool f16 = sb_dtype == TQ_F16;
+  constexpr int NW = kP7Waves, NT = kP7Waves * 64;
   if (f16) {
-    if (G == 1) polar7_sdpa_kernel<1, __half><<<grid, 256, 0, s>>>(p, k);
-    else polar7_sdpa_kernel<2, __half><<<grid, 256, 0, s>>>(p, k);
+    if (G == 1) polar7_sdpa_kernel<1, __half, NW><<<grid, NT, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<2, __half, NW><<<grid, NT, 0, s>>>(p, k);
   } else {
-    if (G == 1) polar7_sdpa_kernel<1, float><<<grid, 256, 0, s>>>(p, k);
-    else polar7_sdpa_kernel<2, float><<<grid, 256, 0, s>>>(p, k);
+    if (G == 1) polar7_sdpa_kernel<1, float, NW><<<grid, NT, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<2, float, NW><<<grid, NT, 0, s>>>(p, k);
   }
   TQ_CHECK_LAUNCH("polar7_sdpa_kernel");
   return TQ_OK;
