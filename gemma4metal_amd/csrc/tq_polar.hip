@@ -922,32 +922,33 @@ __device__ __forceinline__ void quarter_sum(float s[G]) {
   }
 }
 
-// Scores only (compressed_score over polar7 keys): four lanes per key, 64
-// keys per pass of a 256-thread workgroup, 1024 keys per workgroup; the next
+// Scores only (compressed_score over polar7 keys): four lanes per key, NT / 4
+// keys per pass of an NT-thread workgroup, 16 passes per workgroup; the next
 // pass's words are loaded while the current pass is scored.  Grid (key
 // blocks, kv heads * head subgroups).
-template <int G>
-__global__ __launch_bounds__(256) void polar7_score_kernel(P7Keys k, int n, int cap, int gqa,
-                                                           int n_sub, float scale) {
+template <int G, int NT>
+__global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int cap, int gqa,
+                                                          int n_sub, float scale) {
+  constexpr int KPP = NT / 4, KPW = 16 * KPP;  // keys per pass, per workgroup
   __shared__ P7Tables<G> T;
   const int hy = blockIdx.y, kvh = hy / n_sub, sub = hy - (hy / n_sub) * n_sub;
   const int h0 = kvh * gqa + sub * G;
-  const int qt = threadIdx.x & 3, key = threadIdx.x >> 2;  // key 0..63 of a pass
-  const int t0 = blockIdx.x * 1024 + key;
+  const int qt = threadIdx.x & 3, key = threadIdx.x >> 2;  // key of a pass
+  const int t0 = blockIdx.x * KPW + key;
   const int last = n - 1;
   const int64_t rowbase = static_cast<int64_t>(kvh) * cap;
-  const int npass = min(16, (n - blockIdx.x * 1024 + 63) / 64);
-  // rows of this workgroup: rowbase + blockIdx.x * 1024 + (0 .. lim)
-  const P7Rows R = p7_rows(k, rowbase + blockIdx.x * 1024);
-  const uint32_t lim = static_cast<uint32_t>(last - blockIdx.x * 1024);
+  const int npass = min(16, (n - blockIdx.x * KPW + KPP - 1) / KPP);
+  // rows of this workgroup: rowbase + blockIdx.x * KPW + (0 .. lim)
+  const P7Rows R = p7_rows(k, rowbase + blockIdx.x * KPW);
+  const uint32_t lim = static_cast<uint32_t>(last - blockIdx.x * KPW);
   P7Quarter A, B;
   load_p7_quarter(R, min(static_cast<uint32_t>(key), lim), qt, A);
-  load_p7_tables<G, 256>(T, k, h0);
+  load_p7_tables<G, NT>(T, k, h0);
   auto pass = [&](const P7Quarter& Q, int r) {
     float s[G];
     p7_quarter_score<G>(T, Q, qt, scale, s);
     quarter_sum<G>(s);
-    const int t = t0 + 64 * r;
+    const int t = t0 + KPP * r;
     if (qt < G && t < n) {
       float v = s[0];
 #pragma unroll
@@ -956,9 +957,9 @@ __global__ __launch_bounds__(256) void polar7_score_kernel(P7Keys k, int n, int 
     }
   };
   for (int r = 0; r < npass; r += 2) {
-    load_p7_quarter(R, min(static_cast<uint32_t>(key + 64 * (r + 1)), lim), qt, B);
+    load_p7_quarter(R, min(static_cast<uint32_t>(key + KPP * (r + 1)), lim), qt, B);
     pass(A, r);
-    load_p7_quarter(R, min(static_cast<uint32_t>(key + 64 * (r + 2)), lim), qt, A);
+    load_p7_quarter(R, min(static_cast<uint32_t>(key + KPP * (r + 2)), lim), qt, A);
     if (r + 1 < npass) pass(B, r + 1);
   }
 }
@@ -1653,10 +1654,13 @@ int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_
   k.scores = scores;
   const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, kP7MaxG), n_sub = gqa / G;
   TQ_CHECK_ARG(num_kv_heads * n_sub <= 65535, "%s: too many heads", fn);
-  dim3 grid((kv_len + 1023) / 1024, num_kv_heads * n_sub);
+  // 512 threads (two waves per SIMD), 2048 keys per workgroup: the staged
+  // query tables are paid once per 2048 keys
+  constexpr int NT = 512, KPW = 16 * NT / 4;
+  dim3 grid((kv_len + KPW - 1) / KPW, num_kv_heads * n_sub);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (G == 1) polar7_score_kernel<1><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
-  else polar7_score_kernel<2><<<grid, 256, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  if (G == 1) polar7_score_kernel<1, NT><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  else polar7_score_kernel<2, NT><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
   TQ_CHECK_LAUNCH("polar7_score_kernel");
   return TQ_OK;
 }
