@@ -683,8 +683,8 @@ struct P7Keys {
   float* scores;          // [Hq][n] (score only)
 };
 
-// Per-workgroup LDS tables (every entry of t1 / tq / U multiplied by the
-// score scale):
+// Per-workgroup LDS tables (unscaled; the score scale multiplies each key's
+// total):
 //   t1[g][j][c] = q'[2j] cos c1_c + q'[2j+1] sin c1_c  (level 1, per head)
 //   tq[g][pos][b] = sum of (S q')_{8 pos + i} over the set bits i of b
 //   t2[kp | k0 << 2 | k1 << 4] = the four grandchild factors of a level pair
