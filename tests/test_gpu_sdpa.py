@@ -167,6 +167,18 @@ def test_sdpa_d512_gqa8(gpu, Hq, Hkv, L, W, qdt):
     assert_close(host(out), ref, f"D512 Hq{Hq} Hkv{Hkv} L{L} W{W}")
 
 
+@pytest.mark.parametrize("L", [2, 31, 32, 33, 100, 127, 128, 129, 255, 257, 383, 640, 1000])
+def test_sdpa_d512_gqa8_lengths(gpu, L):
+    """The wave-specialised D=512 kernel at lengths that give one split with
+    odd / even step counts and key streams with no keys."""
+    rng = np.random.default_rng(4000 + L)
+    Hq, Hkv = 16, 2
+    qd, qv = queries(rng, (Hq, 512), "bf16")
+    c = host_cache(rng, Hkv, L, 512, "f16")
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], 8)
+    assert_close(host(out), O.sdpa_int4(qv, *c, 8), f"D512 L{L}")
+
+
 def test_sdpa_d512_gqa8_ragged(gpu):
     rng = np.random.default_rng(51)
     B, Hq, Hkv, D, cap = 3, 32, 4, 512, 1500
