@@ -421,6 +421,29 @@ def test_prefill_tile_kernels_agree(gpu, monkeypatch, D, gqa):
     assert_close(ws, O.sdpa_int4_prefill(qv, *c, prior, gqa, 1.0, W), f"ws prefill D{D}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,L", [(32, 16, 256, 3000), (8, 2, 128, 1500), (8, 4, 512, 700)])
+def test_valu_kernel_forced_matches_oracle(gpu, monkeypatch, Hq, Hkv, D, L):
+    """TQ_SDPA_IMPL=valu runs the VALU kernel for fp16 caches too."""
+    rng = np.random.default_rng(D + L)
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    c = host_cache(rng, Hkv, L, D, "f16")
+    monkeypatch.setenv("TQ_SDPA_IMPL", "valu")
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv)
+    assert_close(host(out), O.sdpa_int4(qv, *c, Hq // Hkv), f"valu D{D} L{L}")
+
+
+@pytest.mark.parametrize("chunk", [128, 384, 4096])
+def test_forced_chunk_matches_oracle(gpu, monkeypatch, chunk):
+    """TQ_SDPA_CHUNK overrides the split planner (more or fewer splits)."""
+    rng = np.random.default_rng(chunk)
+    Hq, Hkv, D, L = 32, 16, 256, 6000
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    c = host_cache(rng, Hkv, L, D, "f16")
+    monkeypatch.setenv("TQ_SDPA_CHUNK", str(chunk))
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], 2)
+    assert_close(host(out), O.sdpa_int4(qv, *c, 2), f"chunk {chunk}")
+
+
 def test_sdpa_prefill_tile_and_split_paths_agree(gpu, monkeypatch):
     rng = np.random.default_rng(91)
     Hq, Hkv, D, S, prior, W = 32, 16, 256, 160, 500, 300
