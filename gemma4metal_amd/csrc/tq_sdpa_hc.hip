@@ -107,7 +107,7 @@ __device__ __forceinline__ float hc_half(uint32_t w, int hi) {
 }
 
 // Prologue of both kernels: the scaled q of the 8 heads (qv[k] = element
-// threadIdx.x + kNT k of the 8 x 512 block) as 22-bit fixed point, scattered
+// threadIdx.x + kNT k of the 8 x 512 block) as 21-bit fixed point, scattered
 // into the block-diagonal B images of the K.q products (bq_lds, whose
 // off-diagonal blocks are zeroed here), the per-(head, group) sums of the
 // fixed-point q (sh_qhat) and the per-head exponent F (sh_F).  NW = waves of
@@ -152,7 +152,10 @@ __device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT],
       for (int w2 = 0; w2 < NW; ++w2) hm = fmaxf(hm, red_max[h * KPH + k2][w2]);
     int ex = 0;
     if (hm > 0.0f) frexpf(hm, &ex);  // hm < 2^ex
-    sh_F[h] = 22 - ex;               // |round(q * 2^F)| <= 2^22
+    // |round(q * 2^F)| <= 2^21: the top base-256 digit is then within
+    // [-32, 32], and a group's dot sum_d nibble_d * X_d (|.| <= 64 * 15 *
+    // 2^21 < 2^31) is exact in int32
+    sh_F[h] = 21 - ex;
   }
   __syncthreads();
   uint8_t* bq_bytes = reinterpret_cast<uint8_t*>(&bq_lds[0][0][0]);
@@ -179,7 +182,7 @@ __device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT],
     bq_bytes[o + NG * 64 * 16] = static_cast<uint8_t>(d1);
     bq_bytes[o + 2 * NG * 64 * 16] = static_cast<uint8_t>(d2);
   }
-  // per (head, quant group) sums of the fixed-point q, exact: 64 * 2^22 < 2^31
+  // per (head, quant group) sums of the fixed-point q, exact: 64 * 2^21 < 2^31
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1)
 #pragma unroll
@@ -252,7 +255,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- prologue: q of the 8 heads as 22-bit fixed point, B images in LDS --
+  // ---- prologue: q of the 8 heads as 21-bit fixed point, B images in LDS --
   float qv[NE];
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
@@ -331,8 +334,8 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
-          const int lo01 = acc0[i] + (acc1[i] << 8);
-          const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc2[i]);
+          // the three digits' products, exact in int32
+          const float dot = static_cast<float>(acc0[i] + (acc1[i] << 8) + (acc2[i] << 16));
           const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
           sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
         }
@@ -627,8 +630,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
           const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[s][1][gl][8 * tile + 2 * c]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int lo01 = acc0[i] + (acc1[i] << 8);
-            const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc2[i]);
+            const float dot = static_cast<float>(acc0[i] + (acc1[i] << 8) + (acc2[i] << 16));
             const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
             sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
           }
