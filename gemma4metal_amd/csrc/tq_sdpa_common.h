@@ -155,6 +155,28 @@ __device__ __forceinline__ float merge_factor(float m, float M) {
 // then runs about once per wave instead of whenever the max grows.
 constexpr float kLazyMax = 8.0f;
 
+// Issue pacing of 8-wave workgroups with a static key stream per wave.
+// Waves w and w ^ 4 share a SIMD, whose arbiter favours the older wave: left
+// alone, waves 0-3 finish their (equal) streams long before waves 4-7 (at
+// 256k keys per head: 142 vs 189 us), the CU streaming with half its loads
+// in flight in between.  After each iteration a wave publishes its count in
+// `done_lds` (one int per wave, zeroed before the workgroup's first barrier)
+// and takes the higher issue priority while it is behind its SIMD partner,
+// or level with it and the younger of the two.  Only issue order changes,
+// so results do not depend on timing.
+template <int NW>
+__device__ __forceinline__ void pace_waves(int* done_lds, int wv, int lane, int done) {
+  if constexpr (NW == 8) {
+    if (lane == 0) __hip_atomic_store(&done_lds[wv], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int other = __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(&done_lds[wv ^ (NW / 2)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (other > done || (other == done && wv >= NW / 2))
+      __builtin_amdgcn_s_setprio(1);
+    else
+      __builtin_amdgcn_s_setprio(0);
+  }
+}
+
 // LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G], later
 // reused for the per-split (m, l) of the last workgroup.  NW = partial
 // results per workgroup (one per wave, or per key stream), NT = threads.

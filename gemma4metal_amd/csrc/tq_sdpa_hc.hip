@@ -122,16 +122,10 @@ __device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT],
   // slot (k, w) = elements 64 w + kNT k + lane: one quant group of head
   // (kNT k) / D (kNT divides D, so k alone names the head)
   constexpr int KPH = D / kNT;  // slots k per head
-  // the NE wave reductions step through the shuffle offsets together, so
-  // their LDS round trips overlap
   {
     float mx[NE];
 #pragma unroll
-    for (int k = 0; k < NE; ++k) mx[k] = fabsf(qv[k]);
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1)
-#pragma unroll
-      for (int k = 0; k < NE; ++k) mx[k] = fmaxf(mx[k], shfl_xor_f(mx[k], off));
+    for (int k = 0; k < NE; ++k) mx[k] = wave_max_dpp(fabsf(qv[k]));
     if (lane == 0) {
 #pragma unroll
       for (int k = 0; k < NE; ++k) red_max[k][wave] = mx[k];
@@ -184,9 +178,7 @@ __device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT],
   }
   // per (head, quant group) sums of the fixed-point q, exact: 64 * 2^21 < 2^31
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1)
-#pragma unroll
-    for (int k = 0; k < NE; ++k) X[k] += __shfl_xor(X[k], off, 64);
+  for (int k = 0; k < NE; ++k) X[k] = wave_sum_dpp(X[k]);
   if (lane == 0) {
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
@@ -216,7 +208,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   const int t_end = rg.t_end;
 
   using Fin = Finalize<G, D, NW>;
-  __shared__ float arena[Fin::kArena];
+  __shared__ __attribute__((aligned(16))) float arena[Fin::kArena];
   __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][2 pair + half][lane]
   __shared__ uint32_t sc_lds[NW][4][NG][16];    // [wave][array][group][key pair] fp16 x 2
   __shared__ float red_max[NE][NW];
@@ -459,9 +451,12 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     for (int blk = 0; blk < 4; ++blk) {
       const float off = bacc[blk] - 128.0f * wsum[blk];
 #pragma unroll
-      for (int f = 0; f < 8; ++f)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[8 * (16 * blk + 4 * c + i) + f] = cv[blk][f][i] + off;
+      for (int i = 0; i < 4; ++i) {
+        // dims 8 (16 blk + 4c + i) + f, f = 0..7: two 16-byte stores
+        float4* dst = reinterpret_cast<float4*>(o + 8 * (16 * blk + 4 * c + i));
+        dst[0] = make_float4(cv[blk][0][i] + off, cv[blk][1][i] + off, cv[blk][2][i] + off, cv[blk][3][i] + off);
+        dst[1] = make_float4(cv[blk][4][i] + off, cv[blk][5][i] + off, cv[blk][6][i] + off, cv[blk][7][i] + off);
+      }
     }
   }
   if (c == 0 && m < 8) {
@@ -804,9 +799,12 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       for (int blk = 0; blk < 4; ++blk) {
         const float off = off_lds[s][blk][m];
 #pragma unroll
-        for (int ff = 0; ff < 8; ++ff)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[8 * (16 * blk + 4 * c + i) + ff] = cv[blk][ff][i] + off;
+        for (int i = 0; i < 4; ++i) {
+          // dims 8 (16 blk + 4c + i) + ff, ff = 0..7: two 16-byte stores
+          float4* dst = reinterpret_cast<float4*>(o + 8 * (16 * blk + 4 * c + i));
+          dst[0] = make_float4(cv[blk][0][i] + off, cv[blk][1][i] + off, cv[blk][2][i] + off, cv[blk][3][i] + off);
+          dst[1] = make_float4(cv[blk][4][i] + off, cv[blk][5][i] + off, cv[blk][6][i] + off, cv[blk][7][i] + off);
+        }
       }
     }
   }

@@ -137,18 +137,6 @@ __device__ __forceinline__ float half_hi(uint32_t w) {
   return __half2float(__ushort_as_half(static_cast<uint16_t>(w >> 16)));
 }
 
-// Wave-wide reductions (64 lanes), result in every lane.
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor_f(v, off));
-  return v;
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 // D = 512: 4-wave workgroups at one wave per SIMD (VGPRs + AGPRs for the
 // doubled K buffers and scales).
 // kQG: prefill with query groups -- the G column sets are G / p.pq heads x
@@ -197,6 +185,8 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   __shared__ float red_max[NE][NW];
   __shared__ float sh_qhat[G][NG];
   __shared__ int sh_F[G];
+  __shared__ int s_done[NW];  // iterations processed, per wave (issue pacing)
+  if ((threadIdx.x & 63) == 0) s_done[threadIdx.x >> 6] = 0;
 
   // ---- first loads, issued before the prologue to overlap its latency ------
   const int64_t row0 = (static_cast<int64_t>(cache_batch(p, b)) * p.Hkv + kvh) * p.cap;
@@ -266,7 +256,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   }
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
-    const float mx = wave_max(fabsf(qv[k]));
+    const float mx = wave_max_dpp(fabsf(qv[k]));
     if (lane == 0) red_max[k][wave] = mx;
   }
   {
@@ -307,7 +297,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       bk_bytes[byte0] = static_cast<uint8_t>(d0);
       bk_bytes[byte0 + KM * 64 * 16] = static_cast<uint8_t>(d1);
       bk_bytes[byte0 + 2 * KM * 64 * 16] = static_cast<uint8_t>(d2);
-      const int gsum = wave_sum_i(X);  // exact: 64 * 2^22 < 2^31
+      const int gsum = wave_sum_dpp(X);  // exact: 64 * 2^22 < 2^31
       if (lane == 0) {
         sh_qhat[h][d >> 6] = static_cast<float>(gsum) * ldexpf(1.0f, -F);
         if ((d >> 6) == 0) sh_F[h] = F;
@@ -461,14 +451,18 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     load_iter<D, G>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c, vhalf);
   };
 
+  auto pace = [&](int done) { pace_waves<NW>(s_done, wv, lane, done); };
+  pace(0);
   for (int it = 0; it < nit; it += 2) {
     load_next(bufB, base0 + (it + 1) * kIter);
     __builtin_amdgcn_sched_barrier(0);
     process(bufA, base0 + it * kIter);
+    pace(it + 1);
     __builtin_amdgcn_sched_barrier(0);
     load_next(bufA, base0 + (it + 2) * kIter);
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < nit) process(bufB, base0 + (it + 1) * kIter);
+    pace(it + 2);
     __builtin_amdgcn_sched_barrier(0);
   }
 
