@@ -453,7 +453,12 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 
   auto pace = [&](int done) { pace_waves<NW>(s_done, wv, lane, done); };
   pace(0);
-  for (int it = 0; it < nit; it += 2) {
+  // Steady state: every load in the body is for an iteration of this wave.
+  // The last one or two iterations are peeled, so no load is issued past
+  // the stream: the registers of such a load would have to be waited for
+  // before their reuse after the loop, a full memory round trip per wave.
+  int it = 0;
+  for (; it + 2 < nit; it += 2) {
     load_next(bufB, base0 + (it + 1) * kIter);
     __builtin_amdgcn_sched_barrier(0);
     process(bufA, base0 + it * kIter);
@@ -461,9 +466,18 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     __builtin_amdgcn_sched_barrier(0);
     load_next(bufA, base0 + (it + 2) * kIter);
     __builtin_amdgcn_sched_barrier(0);
-    if (it + 1 < nit) process(bufB, base0 + (it + 1) * kIter);
+    process(bufB, base0 + (it + 1) * kIter);
     pace(it + 2);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if (it + 1 < nit) {
+    load_next(bufB, base0 + (it + 1) * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    process(bufA, base0 + it * kIter);
+    __builtin_amdgcn_sched_barrier(0);
+    process(bufB, base0 + (it + 1) * kIter);
+  } else if (it < nit) {
+    process(bufA, base0 + it * kIter);
   }
 
   // ---- per-wave result into the finalisation arena --------------------------
