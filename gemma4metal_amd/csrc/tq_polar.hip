@@ -430,6 +430,7 @@ __global__ __launch_bounds__(256) void polar16_score_kernel(Attn16 a, int n, int
 // dimensions, output acc / (l + 1e-8).
 template <int D, int G, bool kPacked>
 __global__ __launch_bounds__(256) void polar16_sdpa_kernel(SdpaParams p, Attn16 a) {
+  pin_args(p);
   constexpr int NW = 4, VE = D / 64;
   __shared__ float2 cst[1024];
   __shared__ __align__(16) float qs[G * D];
@@ -1002,6 +1003,8 @@ constexpr int kP7Waves = 8;
 
 template <int G, typename SB, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
+  pin_args(p);
+  asm volatile("" ::"s"(k.qtab), "s"(k.cs), "s"(k.angles), "s"(k.norms), "s"(k.qjl));
   constexpr int D = 128;
   __shared__ P7Tables<G> T;
   using Fin = Finalize<G, D, NW>;

@@ -125,6 +125,7 @@ template <int D>
 __global__ __launch_bounds__(kPfThreads)
 __attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void prefill_int4_kernel(SdpaParams p) {
+  pin_args(p);
   using Gm = PfGeom<D>;
   constexpr int W = Gm::W, KSTR = Gm::KSTR, VSTR = Gm::VSTR, CH = Gm::CH, DB = Gm::DB;
   constexpr int KPT = Gm::KPT;
@@ -305,6 +306,7 @@ void prefill_int4_kernel(SdpaParams p) {
 template <int D>
 __global__ __launch_bounds__(2 * kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_int4_ws_kernel(SdpaParams p) {
+  pin_args(p);
   using Gm = PfGeom<D>;
   constexpr int W = Gm::W, KSTR = Gm::KSTR, VSTR = Gm::VSTR, CH = Gm::CH, DB = Gm::DB;
   constexpr int KPT = Gm::KPT;

@@ -57,7 +57,13 @@ __device__ __forceinline__ void load8(const void* x, int dtype, int64_t off, flo
 
 template <typename SB>
 __global__ __launch_bounds__(256) void quantize_int4_kernel(QuantParams p) {
-  const QuantJob J = p.job[blockIdx.y];
+  // every argument in one batch of scalar loads (one memory round trip),
+  // the job picked by a select rather than a load indexed by blockIdx.y
+  asm volatile("" ::"s"(p.job[0].x), "s"(p.job[0].wq), "s"(p.job[0].s), "s"(p.job[0].b),
+               "s"(p.job[1].x), "s"(p.job[1].wq), "s"(p.job[1].s), "s"(p.job[1].b),
+               "s"(p.x_dtype), "s"(p.rows), "s"(p.dim), "s"(p.mode), "s"(p.pos), "s"(p.heads),
+               "s"(p.n_new), "s"(p.cap), "s"(p.ring));
+  const QuantJob J = blockIdx.y ? p.job[1] : p.job[0];
   const int wpr = p.dim >> 3;  // words per row
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   const int64_t row = gid / wpr;

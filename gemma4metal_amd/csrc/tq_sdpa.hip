@@ -184,6 +184,7 @@ __device__ __forceinline__ void unpack8(uint32_t w, float n[8]) {
 
 template <int D, int G, typename SB>
 __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
+  pin_args(p);
   using Gm = Geom<D, G>;
   constexpr int E = Gm::E, LPT = Gm::LPT, TPS = Gm::TPS, WPL = Gm::WPL, NG = Gm::NG;
   constexpr int RW = D / 8;  // packed words per row

@@ -54,6 +54,20 @@ struct SdpaParams {
   int nq;
 };
 
+// Kernel arguments arrive through scalar loads from the kernarg segment, one
+// memory round trip per batch of loads.  Left to itself, the compiler places
+// each field's load near its first use: behind the split-range arithmetic
+// and its early exit, that made three dependent round trips before the
+// first K/V load could issue (1.3 us after a wave's start at L = 786).
+// Pinning the fields the prologue needs into SGPRs at kernel entry issues
+// them as one batch.
+__device__ __forceinline__ void pin_args(const SdpaParams& p) {
+  asm volatile("" ::"s"(p.q), "s"(p.kq), "s"(p.ks), "s"(p.kb), "s"(p.vq), "s"(p.vs), "s"(p.vb),
+               "s"(p.seq_lens), "s"(p.windows), "s"(p.q_dtype), "s"(p.Hq), "s"(p.Hkv), "s"(p.cap),
+               "s"(p.gqa), "s"(p.n_sub), "s"(p.n), "s"(p.window), "s"(p.n_clamp),
+               "s"(p.scale_log2), "s"(p.chunk), "s"(p.prefill));
+}
+
 // Batch index of the cache that batch element b reads.
 __device__ __forceinline__ int cache_batch(const SdpaParams& p, int b) { return p.prefill ? 0 : b; }
 

@@ -191,6 +191,7 @@ __device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT],
 
 __global__ __launch_bounds__(kHcWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void sdpa_int4_hc_kernel(SdpaParams p) {
+  pin_args(p);
   constexpr int NW = kHcWaves, D = kHcD, G = kHcG, NG = kHcNG;
   constexpr int kNT = NW * 64;
   constexpr int kIter = 32 * NW;          // keys per workgroup iteration
@@ -488,6 +489,7 @@ constexpr int kHs = 4;  // key streams (producer / consumer pairs)
 
 __global__ __launch_bounds__(2 * kHs * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_int4_hc2_kernel(SdpaParams p) {
+  pin_args(p);
   constexpr int NS = kHs, NWV = 2 * kHs, D = kHcD, G = kHcG, NG = kHcNG;
   constexpr int kNT = NWV * 64;
   constexpr int kIter = 32 * NS;   // keys per workgroup iteration
@@ -819,6 +821,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 // partials come from an earlier kernel, so plain loads see them.  Grid
 // (ceil(Hq * D / 4 / 16), batch).
 __global__ __launch_bounds__(256) void merge_splits_kernel(SdpaParams p, int D) {
+  pin_args(p);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sl = lane & 15;
   const int D4 = D / 4;

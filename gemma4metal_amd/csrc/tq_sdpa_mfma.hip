@@ -155,6 +155,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   constexpr int RW = D / 8;
   constexpr int NE = (G * D + kNT - 1) / kNT;  // q elements per thread
 
+  pin_args(p);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;  // A row / B,C column; lane group
   const int n = m;                         // this lane's (head, group) column
