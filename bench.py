@@ -80,9 +80,29 @@ def gen_q(torch, shape, gen):
     return q.to(torch.bfloat16)
 
 
+PREWARM_S = 0.25  # seconds of untimed steps before the warmup steps
+
+
+def prewarm(torch, fn, seconds=PREWARM_S):
+    """Runs fn back to back for `seconds` of wall time, untimed.  The GPU
+    leaves its idle clocks only after some milliseconds under load, and a
+    timed region of a few ms (100 launches of ~35 us) right after process
+    start would otherwise measure part of that ramp: the same 32k layer read
+    34-37 us timed first in a process and 32.4 us timed after other work."""
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(16):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def time_launches(torch, fn, steps, warmup):
     """(whole-region ms per step, mean per-launch ms) with HIP events on the
-    current stream -- the stream every launch is issued on."""
+    current stream -- the stream every launch is issued on.  A time-based
+    pre-warm and then `warmup` untimed steps come first."""
+    prewarm(torch, fn)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
