@@ -263,32 +263,45 @@ struct Finalize {
     __syncthreads();
     if (!s_last) return;
 
-    // Stage every split's (m, l) in LDS, then each thread reduces its
-    // (head, dim) outputs with independent coherent loads.
-    float* s_m = arena;  // the wave-merge data is dead past the barriers above
-    float* s_l = arena + G * kMaxSplits;
-    for (int i = threadIdx.x; i < G * S; i += kNT) {
-      const int h = i / S, sp = i - (i / S) * S;
-      if (h >= nvalid) continue;
-      const int64_t slot = row(h) * p.max_splits + sp;
-      s_m[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2);
-      s_l[h * kMaxSplits + sp] = load_coherent(p.ws_ml + slot * 2 + 1);
-    }
-    __syncthreads();
+    // Each thread merges its (head, dim) outputs, KC splits at a time.  A
+    // wave's outputs share one head (64 divides D), so lane k loads split
+    // s0 + k's (m, l) and v_readlane hands them to the whole wave; those two
+    // loads and the KC partial loads (coalesced over dims) all go out before
+    // the first use: one memory round trip per chunk, one in all for S <= KC.
+    constexpr int KC = 16;
+    static_assert(D % 64 == 0, "one head per wave");
+    const int lane = threadIdx.x & 63;
     for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
       const int h = idx / D, d = idx - (idx / D) * D;
-      if (h >= nvalid) continue;
-      const float* ms = s_m + h * kMaxSplits;
-      const float* ls = s_l + h * kMaxSplits;
-      float M = -INFINITY;
-      for (int sp = 0; sp < S; ++sp) M = fmaxf(M, ms[sp]);
+      if (h >= nvalid) continue;  // wave-uniform
+      const float* ml = p.ws_ml + row(h) * p.max_splits * 2;
       const float* po = p.ws_o + row(h) * p.max_splits * D + d;
-      float O = 0.0f, Ls = 0.0f;
-#pragma unroll 8
-      for (int sp = 0; sp < S; ++sp) {
-        const float f = merge_factor(ms[sp], M);
-        O = fmaf(load_coherent(po + static_cast<int64_t>(sp) * D), f, O);
-        Ls = fmaf(ls[sp], f, Ls);
+      float M = -INFINITY, Ls = 0.0f, O = 0.0f;
+      for (int s0 = 0; s0 < S; s0 += KC) {
+        const int sl = min(s0 + (lane & (KC - 1)), S - 1);
+        const float mv = load_coherent(ml + 2 * sl);
+        const float lv = load_coherent(ml + 2 * sl + 1);
+        float ok[KC];
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+          ok[k] = load_coherent(po + static_cast<int64_t>(min(s0 + k, S - 1)) * D);
+        float mk[KC], Mn = M;
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          mk[k] = s0 + k < S ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mv), k))
+                             : -INFINITY;
+          Mn = fmaxf(Mn, mk[k]);
+        }
+        const float fr = merge_factor(M, Mn);
+        Ls *= fr;
+        O *= fr;
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          const float f = merge_factor(mk[k], Mn);
+          Ls = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), k)), f, Ls);
+          O = fmaf(ok[k], f, O);
+        }
+        M = Mn;
       }
       p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
     }
