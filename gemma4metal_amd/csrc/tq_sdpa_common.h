@@ -13,7 +13,10 @@ namespace tq {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kMaxSplits = 256;  // splits per (sequence, kv head); bounds the merge's LDS
+constexpr int kMaxSplits = 256;  // splits per (sequence, kv head)
+// Split counters at the head of the workspace (ints); batch * num_heads of
+// them are in use at once.
+constexpr int64_t kMaxCounters = 1 << 16;
 
 struct SdpaParams {
   const void* q;
@@ -252,7 +255,13 @@ struct Finalize {
     __syncthreads();
     __shared__ int s_last;
     if (threadIdx.x == 0) {
-      int* cnt = p.ws_cnt + counter;
+      // Counter `counter` (< gridDim.z * Hq, checked on the host) sits up to
+      // 32 ints (one 128 B line) from its neighbours, as far as the region
+      // allows: the atomics of every head's last splits arrive together at
+      // the end of a launch, and on one shared line they serialise.
+      const int64_t ncnt = static_cast<int64_t>(gridDim.z) * p.Hq;
+      const int stride = static_cast<int>(min(int64_t{32}, kMaxCounters / ncnt));
+      int* cnt = p.ws_cnt + static_cast<int64_t>(counter) * stride;
       const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = (old == S - 1);
       // leave the workspace zeroed for the next call -- with an atomic RMW,
@@ -313,7 +322,6 @@ struct Finalize {
 // region has a FIXED size at offset 0 so that no call's partials ever overlap
 // another call's counters: counters must read zero on entry (the kernels
 // return every counter they use to zero), whatever shapes earlier calls had.
-constexpr int64_t kMaxCounters = 1 << 16;  // batch * num_heads
 
 struct WsLayout {
   size_t cnt_off, ml_off, o_off, total;
