@@ -134,8 +134,12 @@ def test_workspace_reuse_across_shapes(gpu):
     correct in any order."""
     rng = np.random.default_rng(41)
     cases = []
+    # the last case has batch * heads = 2560 > 2048, so its split counters
+    # are closer than one line apart (stride 25 ints instead of 32)
+    many = rng.integers(1, 49, size=80).tolist()
     for (B, cap, lens, wins) in [(2, 900, [900, 513], [0, 0]), (3, 1500, [1500, 7, 1025], [1024, 0, 0]),
-                                 (1, 4000, [4000], [0]), (4, 700, [1, 700, 650, 129], [0, 64, 0, 0])]:
+                                 (1, 4000, [4000], [0]), (4, 700, [1, 700, 650, 129], [0, 64, 0, 0]),
+                                 (80, 48, many, [0] * 80)]:
         qd, qv = queries(rng, (B, 32, 256), "bf16")
         k = O.rms_norm(rng.standard_normal((B, 16, cap, 256)).astype(np.float32))
         v = rng.standard_normal((B, 16, cap, 256)).astype(np.float32)
@@ -144,7 +148,7 @@ def test_workspace_reuse_across_shapes(gpu):
         cases.append((qd, [dev(a) for a in c], dev(np.array(lens, np.int32)),
                       dev(np.array(wins, np.int32)), ref))
     for rep in range(3):
-        for i in (0, 2, 1, 3, 2, 0):
+        for i in (0, 2, 4, 1, 3, 4, 2, 0):
             qd, cd, ld, wd, ref = cases[i]
             out = gpu.sdpa_int4_ragged(qd, *cd, ld, 2, windows=wd)
             assert_close(host(out), ref, f"rep {rep} case {i}")
