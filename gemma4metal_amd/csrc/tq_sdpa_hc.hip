@@ -15,9 +15,10 @@
 //   columns 8-15 over group 2P + 1's, zero elsewhere; two such products
 //   (dims 0-31, 32-63 of each group) accumulate into one C.  q is three
 //   signed base-256 digits of round(q * 2^F), so C[key][column] is the exact
-//   integer dot of one group.  A lane adds s_g * 2^-F * dot_g + b_g *
-//   sum(q over g) for its column's group; one cross-lane add (column n and
-//   n ^ 8) then gives the score of head n % 8 in both columns.
+//   integer dot of one group.  A lane adds s_g * dot_g + b_g * sum(q * 2^F
+//   over g) for its column's group; one cross-lane add (column n and n ^ 8)
+//   and one multiply by 2^-F then give the score of head n % 8 in both
+//   columns.
 // P . V  -- v_mfma_f32_16x16x32_bf16 per block of 16 V words (2 quant
 //   groups): A = (128 + nibble) as bf16 of 16 words x 32 keys (v_perm_b32 +
 //   and-or), B = the bf16 hi / lo split of p * s_v in columns (head, group of
@@ -263,7 +264,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   // q sums of this lane's column: head hh, group 2P + m / 8 of pair P
   float qh[NG / 2];
 #pragma unroll
-  for (int P = 0; P < NG / 2; ++P) qh[P] = sh_qhat[hh][2 * P + (m >> 3)];
+  for (int P = 0; P < NG / 2; ++P) qh[P] = sh_qhat[hh][2 * P + (m >> 3)] * ldexpf(1.0f, sh_F[hh]);
 
   // ---- main loop ----------------------------------------------------------
   float m_run = -INFINITY, l_run = 0.0f;
@@ -326,11 +327,10 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
         const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[wv][1][gl][8 * tile + 2 * c]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
-          // the three digits' products, exact in int32
-          const float dot = static_cast<float>(acc0[i] + (acc1[i] << 8) + (acc2[i] << 16));
+          // the three digits' products, exact in int32 (two shift-adds)
+          const float dot = static_cast<float>((acc2[i] << 16) + ((acc1[i] << 8) + acc0[i]));
           const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
-          sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
+          sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1), fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
         }
       }
     }
@@ -340,7 +340,8 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        sc[tile][i] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false));
+        sc[tile][i] = sf * (sc[tile][i] + __int_as_float(__builtin_amdgcn_mov_dpp(
+                                               __float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false)));
 #pragma unroll
     for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
@@ -574,7 +575,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     const float sf = ldexpf(1.0f, -sh_F[hh]);
     float qh[NG / 2];
 #pragma unroll
-    for (int P = 0; P < NG / 2; ++P) qh[P] = sh_qhat[hh][2 * P + (m >> 3)];
+    for (int P = 0; P < NG / 2; ++P) qh[P] = sh_qhat[hh][2 * P + (m >> 3)] * ldexpf(1.0f, sh_F[hh]);
 
     float m_run = -INFINITY, l_run = 0.0f;
     float wsum[4], bacc[4];
@@ -627,9 +628,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
           const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[s][1][gl][8 * tile + 2 * c]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float dot = static_cast<float>(acc0[i] + (acc1[i] << 8) + (acc2[i] << 16));
+            const float dot = static_cast<float>((acc2[i] << 16) + ((acc1[i] << 8) + acc0[i]));
             const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
-            sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1) * sf, fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
+            sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1), fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
           }
         }
       }
@@ -637,7 +638,8 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          sc[tile][i] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false));
+          sc[tile][i] = sf * (sc[tile][i] + __int_as_float(__builtin_amdgcn_mov_dpp(
+                                                 __float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false)));
           if (t0 + 16 * tile + 4 * c + i >= t_end) sc[tile][i] = -INFINITY;
         }
 
