@@ -196,7 +196,7 @@ def main():
                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4),
                              "traffic": measured_traffic() if L == 32768 else None,
-                             "kernel": "sdpa_int4_mfma_kernel<256,2,8,false>",
+                             "kernel": "sdpa_int4_mfma_kernel<256,2,8,false,true>",
                              "bytes_per_launch": nbytes,
                              "us_per_launch": round(ms_step * 1e3, 2),
                              "us_per_launch_event_bracketed_mean": round(ms_launch * 1e3, 2),
