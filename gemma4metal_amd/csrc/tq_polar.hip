@@ -738,35 +738,53 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
 // q' = P q (or q), u = S q', and the tables of one head.  Grid (heads,
 // kP7PrepParts): the workgroups of a head each recompute q' and u (two
 // 128 x 128 products, two threads per output) and write their share of the
-// tables.  The rows of P and S are loaded before the first wait.
+// tables.  P and S are staged in LDS with coalesced loads (consecutive
+// threads, consecutive 16 B: a workgroup load instruction covers 4 KB),
+// all issued before the first wait; rows are padded to kPrepRS floats.
+// (Loading each thread's own half row straight into registers made every
+// load instruction touch 64 separate lines.)
 constexpr int kP7PrepParts = 4;
+constexpr int kPrepRS = 132;
 __global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, const float* P,
                                                              const float* S, const float* cs,
                                                              float* qtab, float* q_rot,
                                                              float* q_sketch) {
+  __shared__ __attribute__((aligned(16))) float mat[2][128 * kPrepRS];  // P, S
   __shared__ float xs[128], qp[128], u[128], csl[40];
   const int h = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
   const int i = t >> 1, half = t & 1;  // output row, half of its dot product
-  const float4* srow = reinterpret_cast<const float4*>(S + i * 128 + 64 * half);
-  const float4* prow = reinterpret_cast<const float4*>((P ? P : S) + i * 128 + 64 * half);
-  float4 pr[16], sr[16];
+  {
+    // float4 f = 256 c + t of a matrix: row f / 32, columns 4 (f % 32) .. + 3
+    const float4* P4 = reinterpret_cast<const float4*>(P ? P : S);
+    const float4* S4 = reinterpret_cast<const float4*>(S);
+    float4 pv[16], sv[16];
 #pragma unroll
-  for (int c = 0; c < 16; ++c) {
-    pr[c] = prow[c];
-    sr[c] = srow[c];
+    for (int c = 0; c < 16; ++c) {
+      pv[c] = P4[256 * c + t];
+      sv[c] = S4[256 * c + t];
+    }
+    if (t < 128) xs[t] = q[static_cast<int64_t>(h) * 128 + t];
+    if (t < 40) csl[t] = cs[t];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int f = 256 * c + t, at = (f >> 5) * kPrepRS + 4 * (f & 31);
+      *reinterpret_cast<float4*>(&mat[0][at]) = pv[c];
+      *reinterpret_cast<float4*>(&mat[1][at]) = sv[c];
+    }
   }
-  if (t < 128) xs[t] = q[static_cast<int64_t>(h) * 128 + t];
-  if (t < 40) csl[t] = cs[t];
   __syncthreads();
+  const float* prow = &mat[0][i * kPrepRS + 64 * half];
+  const float* srow = &mat[1][i * kPrepRS + 64 * half];
   float acc = 0.0f;
   if (P) {
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
+      const float4 a = *reinterpret_cast<const float4*>(prow + 4 * c);
       const float* x = xs + 64 * half + 4 * c;
-      acc = fmaf(x[0], pr[c].x, acc);
-      acc = fmaf(x[1], pr[c].y, acc);
-      acc = fmaf(x[2], pr[c].z, acc);
-      acc = fmaf(x[3], pr[c].w, acc);
+      acc = fmaf(x[0], a.x, acc);
+      acc = fmaf(x[1], a.y, acc);
+      acc = fmaf(x[2], a.z, acc);
+      acc = fmaf(x[3], a.w, acc);
     }
   } else {
     acc = half == 0 ? xs[i] : 0.0f;
@@ -780,11 +798,12 @@ __global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, con
   float us = 0.0f;
 #pragma unroll
   for (int c = 0; c < 16; ++c) {
+    const float4 a = *reinterpret_cast<const float4*>(srow + 4 * c);
     const float* x = qp + 64 * half + 4 * c;
-    us = fmaf(x[0], sr[c].x, us);
-    us = fmaf(x[1], sr[c].y, us);
-    us = fmaf(x[2], sr[c].z, us);
-    us = fmaf(x[3], sr[c].w, us);
+    us = fmaf(x[0], a.x, us);
+    us = fmaf(x[1], a.y, us);
+    us = fmaf(x[2], a.z, us);
+    us = fmaf(x[3], a.w, us);
   }
   us += shfl_xor_f(us, 1);
   if (half == 0) {
