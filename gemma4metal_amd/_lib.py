@@ -60,6 +60,8 @@ SIGNATURES = {
     "tq_polar7_encode": (I, [P, P, P, P, P, I64, P, P, P, P]),
     "tq_polar7_kv_append": (I, [P, P, P, P, P, P, P, P, I, I, I, P, I, P]),
     "tq_polar7_prepare_query": (I, [P, P, P, P, I, P, P, P, P]),
+    "tq_polar7_sketch_precondition": (I, [P, P, P, P]),
+    "tq_polar7_prepare_query_sp": (I, [P, P, P, P, I, P, P, P, P]),
     "tq_polar7_score": (I, [P, P, P, P, P, I, I, I, I, F, P, P]),
     "tq_polar7_sdpa_workspace_size": (SZ, [I, I, I]),
     "tq_polar7_sdpa_int4v": (I, [P, P, P, P, P, P, P, P, I, P, I, I, I, I, F, I, P, SZ, P]),

@@ -669,10 +669,12 @@ __global__ __launch_bounds__(128) void rotate128_kernel(const float* x, const fl
 
 // ---- polar7 scores ------------------------------------------------------------
 
-// Per-head query tables written by polar7_prepare_kernel, kP7QTab floats per
-// head: t1 [64][16] (level 1: q'[2j] cos c1_k + q'[2j+1] sin c1_k), tq
-// [16][256] (QJL: sum of (S q')_{8 pos + i} over the set bits i of a byte),
-// then U = sum of S q' (and padding to a 16-byte multiple).
+// Per-head query tables written by polar7_prepare_kernel or
+// polar7_prepare_sp_kernel, kP7QTab floats per head: t1 [64][16] (level 1:
+// q'[2j] cos c1_k + q'[2j+1] sin c1_k), tq [16][256] (QJL: sum of
+// (S q')_{8 pos + i} over the set bits i of a byte), then U = sum of S q'
+// as the sum of four floats (partial sums, or U and three zeros) and
+// padding to a 16-byte multiple.
 constexpr int kP7QTab = 1024 + 4096 + 16;
 
 struct P7Keys {
@@ -723,7 +725,7 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
     const float4 v = reinterpret_cast<const float4*>(k.qtab + static_cast<int64_t>(h0 + g) * kP7QTab)[r];
     if (r < 256) reinterpret_cast<float4*>(&T.t1[g][0][0])[p7_t1_row(r >> 2) * 4 + (r & 3)] = v;
     else if (r < 1280) reinterpret_cast<float4*>(&T.tq[g][0][0])[r - 256] = v;
-    else if (r == 1280) T.U[g] = v.x;
+    else if (r == 1280) T.U[g] = (v.x + v.y) + (v.z + v.w);
   }
   if (threadIdx.x < 64) {
     const int kp = threadIdx.x & 3, k0 = (threadIdx.x >> 2) & 3, k1 = threadIdx.x >> 4;
@@ -827,6 +829,104 @@ __global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, con
   if (part == 0 && t < 64) {
     const float sum = wave_sum_f(u[t] + u[t + 64]);
     if (t < 16) out[5120 + t] = t == 0 ? sum : 0.0f;
+  }
+}
+
+// SP = S P (S when P is null): grid 128 rows x 128 threads; thread j reads
+// column j of P, so each k is one coalesced row of P.
+__global__ __launch_bounds__(128) void polar7_sp_kernel(const float* P, const float* S, float* SP) {
+  const int i = blockIdx.x, j = threadIdx.x;
+  const float* srow = S + i * 128;
+  float acc = 0.0f;
+  if (P) {
+#pragma unroll 8
+    for (int k = 0; k < 128; ++k) acc = fmaf(srow[k], P[k * 128 + j], acc);
+  } else {
+    acc = srow[j];
+  }
+  SP[i * 128 + j] = acc;
+}
+
+// The tables of polar7_prepare_kernel from q, P and SP = S P: u = S q' =
+// SP q, so q' and u are independent products of q.  Part `part` of a head
+// computes rows 32 part .. + 31 of both (its share of the tables needs no
+// others: level-1 pairs 16 part .. + 15, QJL bytes 4 part .. + 3), staging
+// just those rows of P and SP (32 KB) in LDS, and writes the partial sum
+// of its u rows to float 5120 + part.
+constexpr int kPrepRows = 128 / kP7PrepParts;
+__global__ __launch_bounds__(256) void polar7_prepare_sp_kernel(const float* q, const float* P,
+                                                                const float* SP, const float* cs,
+                                                                float* qtab, float* q_rot,
+                                                                float* q_sketch) {
+  __shared__ __attribute__((aligned(16))) float mat[2][kPrepRows * kPrepRS];  // rows of P, SP
+  __shared__ float xs[128], qp[128], u[128], csl[40];
+  const int h = blockIdx.x, part = blockIdx.y, t = threadIdx.x;
+  const int r0 = kPrepRows * part;
+  {
+    // float4 f = 256 c + t of the 32-row slab: row f / 32, columns 4 (f % 32) .. + 3
+    const float4* P4 = reinterpret_cast<const float4*>((P ? P : SP) + r0 * 128);
+    const float4* S4 = reinterpret_cast<const float4*>(SP + r0 * 128);
+    float4 pv[4], sv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      pv[c] = P4[256 * c + t];
+      sv[c] = S4[256 * c + t];
+    }
+    if (t < 128) xs[t] = q[static_cast<int64_t>(h) * 128 + t];
+    if (t < 40) csl[t] = cs[t];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int f = 256 * c + t, at = (f >> 5) * kPrepRS + 4 * (f & 31);
+      *reinterpret_cast<float4*>(&mat[0][at]) = pv[c];
+      *reinterpret_cast<float4*>(&mat[1][at]) = sv[c];
+    }
+  }
+  __syncthreads();
+  // outputs o = 0..31: q' row r0 + o; o = 32..63: u row r0 + o - 32; four
+  // threads per output, 32 elements each
+  const int o = t >> 2, qr = t & 3;
+  const float* row = &mat[o >> 5][(o & 31) * kPrepRS + 32 * qr];
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float4 a = *reinterpret_cast<const float4*>(row + 4 * c);
+    const float* x = xs + 32 * qr + 4 * c;
+    acc = fmaf(x[0], a.x, acc);
+    acc = fmaf(x[1], a.y, acc);
+    acc = fmaf(x[2], a.z, acc);
+    acc = fmaf(x[3], a.w, acc);
+  }
+  if (o < 32 && !P) acc = qr == 0 ? xs[r0 + o] : 0.0f;
+  acc += shfl_xor_f(acc, 1);
+  acc += shfl_xor_f(acc, 2);
+  if (qr == 0) {
+    const int r = r0 + (o & 31);
+    if (o < 32) {
+      qp[r] = acc;
+      if (q_rot) q_rot[static_cast<int64_t>(h) * 128 + r] = acc;
+    } else {
+      u[r] = acc;
+      if (q_sketch) q_sketch[static_cast<int64_t>(h) * 128 + r] = acc;
+    }
+  }
+  __syncthreads();
+  float* out = qtab + static_cast<int64_t>(h) * kP7QTab;
+  constexpr int kT1 = 1024 / kP7PrepParts, kTq = 4096 / kP7PrepParts;
+  for (int e = kT1 * part + t; e < kT1 * (part + 1); e += 256) {
+    const int j = e >> 4, c = e & 15;
+    out[e] = qp[2 * j] * csl[2 * c] + qp[2 * j + 1] * csl[2 * c + 1];
+  }
+  for (int e = kTq * part + t; e < kTq * (part + 1); e += 256) {
+    const int pos = e >> 8, bits = e & 255;
+    float sum = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) sum += ((bits >> b) & 1) ? u[8 * pos + b] : 0.0f;
+    out[1024 + e] = sum;
+  }
+  if (t < 64) {
+    const float sum = wave_sum_f(t < kPrepRows ? u[r0 + t] : 0.0f);
+    if (t == 0) out[5120 + part] = sum;
+    if (part == 0 && t >= kP7PrepParts && t < 16) out[5120 + t] = 0.0f;
   }
 }
 
@@ -1659,6 +1759,31 @@ int tq_polar7_prepare_query(const float* q, const float* precondition, const flo
   polar7_prepare_kernel<<<dim3(num_heads, kP7PrepParts), 256, 0, static_cast<hipStream_t>(stream)>>>(
       q, precondition, sketch, cs_tables, q_tables, q_rot, q_sketch);
   TQ_CHECK_LAUNCH("polar7_prepare_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_sketch_precondition(const float* precondition, const float* sketch,
+                                  float* sketch_precondition, void* stream) {
+  const char* fn = "tq_polar7_sketch_precondition";
+  TQ_CHECK_ARG(sketch && sketch_precondition, "%s: null pointer", fn);
+  polar7_sp_kernel<<<128, 128, 0, static_cast<hipStream_t>(stream)>>>(precondition, sketch,
+                                                                      sketch_precondition);
+  TQ_CHECK_LAUNCH("polar7_sp_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_prepare_query_sp(const float* q, const float* precondition,
+                               const float* sketch_precondition, const float* cs_tables,
+                               int num_heads, float* q_tables, float* q_rot, float* q_sketch,
+                               void* stream) {
+  const char* fn = "tq_polar7_prepare_query_sp";
+  TQ_CHECK_ARG(q && sketch_precondition && cs_tables && q_tables, "%s: null pointer", fn);
+  TQ_CHECK_ARG(num_heads >= 0 && num_heads <= 65535, "%s: bad num_heads", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(q_tables) % 16 == 0, "%s: q_tables must be 16-byte aligned", fn);
+  if (num_heads == 0) return TQ_OK;
+  polar7_prepare_sp_kernel<<<dim3(num_heads, kP7PrepParts), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      q, precondition, sketch_precondition, cs_tables, q_tables, q_rot, q_sketch);
+  TQ_CHECK_LAUNCH("polar7_prepare_sp_kernel");
   return TQ_OK;
 }
 

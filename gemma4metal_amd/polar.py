@@ -267,6 +267,10 @@ class Polar7Codec:
         if codebooks is None:
             codebooks, cs_tables = polar7_codebooks(sketch.device)
         self.cb, self.cs = codebooks.contiguous(), cs_tables.contiguous()
+        # S P, so the query sketch S (P q) is one product of q
+        self.SP = torch.empty_like(sketch)
+        call("tq_polar7_sketch_precondition", _ptr(self.P), _ptr(self.S), _ptr(self.SP), _stream(None))
+        torch.cuda.current_stream().synchronize()
 
     def new_cache(self, num_kv_heads: int, capacity: int, batch: Optional[int] = None):
         lead = (num_kv_heads, capacity) if batch is None else (batch, num_kv_heads, capacity)
@@ -310,7 +314,7 @@ class Polar7Codec:
         tab = torch.empty((Hq, P7_QTAB), dtype=torch.float32, device=q.device)
         qp = torch.empty_like(q) if with_vectors else None
         qs = torch.empty_like(q) if with_vectors else None
-        call("tq_polar7_prepare_query", _ptr(q), _ptr(self.P), _ptr(self.S), _ptr(self.cs), Hq,
+        call("tq_polar7_prepare_query_sp", _ptr(q), _ptr(self.P), _ptr(self.SP), _ptr(self.cs), Hq,
              _ptr(tab), _ptr(qp), _ptr(qs), _stream(stream))
         return (tab, qp, qs) if with_vectors else tab
 

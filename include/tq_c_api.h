@@ -291,12 +291,26 @@ int tq_qjl_query(const float* q_rot, const float* sketch, int num_heads, float* 
  * kernels read, TQ_POLAR7_QTAB floats per head in q_tables (16-byte
  * aligned): [64][16] level-1 table q'[2j] cos c_k + q'[2j+1] sin c_k,
  * [16][256] QJL byte table (sum of (S q')_{8 pos + i} over the set bits i),
- * then sum(S q') and padding.  q_rot / q_sketch ([num_heads, 128]) are
- * optional copies of q' and S q' (NULL: not written). */
+ * then sum(S q') as the sum of four floats, and padding.  q_rot / q_sketch
+ * ([num_heads, 128]) are optional copies of q' and S q' (NULL: not
+ * written). */
 #define TQ_POLAR7_QTAB 5136
 int tq_polar7_prepare_query(const float* q, const float* precondition, const float* sketch,
                             const float* cs_tables, int num_heads, float* q_tables, float* q_rot,
                             float* q_sketch, void* stream);
+/* No counterpart in the reference (QJL is this build's addition, README.md:
+ * 11,176): sketch_precondition [128][128] = S P (S when precondition is
+ * NULL), computed once per codec. */
+int tq_polar7_sketch_precondition(const float* precondition, const float* sketch,
+                                  float* sketch_precondition, void* stream);
+/* The same tables as tq_polar7_prepare_query from S P in place of S: S q'
+ * is then (S P) q, a product of q independent of q', so the tables of a
+ * head are built in four parts of 32 rows each, without a second product
+ * pass (no counterpart in the reference, as above). */
+int tq_polar7_prepare_query_sp(const float* q, const float* precondition,
+                               const float* sketch_precondition, const float* cs_tables,
+                               int num_heads, float* q_tables, float* q_rot, float* q_sketch,
+                               void* stream);
 /* scores[h, n] = scale * (<q'_h, yhat_n> + sqrt(pi/2)/128 * ||r_n|| *
  * <S q'_h, sign(S r_n)>) over rows [0, kv_len) of kv head h / gqa. */
 int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_t* norms,

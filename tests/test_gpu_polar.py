@@ -207,7 +207,32 @@ def test_prepare_query(pq):
     bits = (np.arange(256)[:, None] >> np.arange(8)) & 1
     tq = np.einsum("hpi,bi->hpb", qs_ref.reshape(32, 16, 8), bits)
     assert np.max(np.abs(tab[:, 1024:5120].reshape(32, 16, 256) - tq)) < 1e-3
-    assert np.max(np.abs(tab[:, 5120] - qs_ref.sum(1))) < 1e-2
+    # sum of S q' as four partial sums, then zero padding
+    assert np.max(np.abs(tab[:, 5120:5124].sum(1) - qs_ref.sum(1))) < 1e-2
+    assert not tab[:, 5124:].any()
+
+
+@pytest.mark.parametrize("rot", [True, False])
+def test_prepare_query_entry_points_agree(pq, rot):
+    """tq_polar7_prepare_query (S applied to q') and tq_polar7_prepare_query_sp
+    (S P applied to q, the codec's path) give the same tables up to fp32
+    rounding, and S P from tq_polar7_sketch_precondition is S P."""
+    import ctypes
+    from gemma4metal_amd._lib import call
+    rng, _, P, S = p7_inputs(8, 0)
+    q = rng.standard_normal((32, 128)).astype(f32)
+    codec = pq.Polar7Codec(dev(P) if rot else None, dev(S))
+    sp_ref = S.astype(np.float64) @ (P.astype(np.float64) if rot else np.eye(128))
+    assert np.max(np.abs(host(codec.SP) - sp_ref)) < 1e-4
+    qd = dev(q)
+    tab_sp = host(codec.prepare_query(qd))
+    tab = torch.empty((32, pq.P7_QTAB), dtype=torch.float32, device="cuda")
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+    call("tq_polar7_prepare_query", ptr(qd), ptr(codec.P), ptr(codec.S), ptr(codec.cs), 32,
+         ptr(tab), ptr(None), ptr(None), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    tab = host(tab)
+    assert np.max(np.abs(tab[:, :5120] - tab_sp[:, :5120])) < 1e-3
+    assert np.max(np.abs(tab[:, 5120:5124].sum(1) - tab_sp[:, 5120:5124].sum(1))) < 1e-2
 
 
 def p7_cache_on_gpu(pq, seed, Hkv, L, rot=True):
