@@ -75,9 +75,10 @@ int head_subgroup(int gqa) {
 // kv head, head subgroup) groups of max_len keys, never fewer than kMinChunk
 // rows.  A batched (ragged) launch also splits every sequence of max_len into
 // at least min_splits chunks: its sequences differ in length, and a long one
-// in one chunk is the tail of the whole launch.  (Measured on the B=64 ragged
-// workload: 2 beats 1, 4 and 8 -- each split adds a workgroup's fixed
-// prologue / merge cost.)
+// in a few large chunks is the tail of the whole launch.  (Measured on the
+// B=64 ragged workload, ms per step: chunks of max_len/2 0.721, /4 0.664,
+// /5 0.630, /6 0.634, /10 0.646.  Each chunk adds a workgroup's prologue and
+// finalisation, a few us in which its CU does not stream.)
 int plan_chunk(int max_len, int64_t groups, int min_splits) {
   // never more than kMaxSplits chunks per sequence
   const int64_t floor_c = (static_cast<int64_t>(max_len) + kMaxSplits - 1) / kMaxSplits;
@@ -106,7 +107,7 @@ int max_splits_bound(int max_len, int64_t groups, int min_splits) {
 }
 
 // Chunks per sequence of max_len a launch of `batch` sequences uses at least.
-int min_splits_for(int batch) { return batch > 1 ? 2 : 1; }
+int min_splits_for(int batch) { return batch > 1 ? 5 : 1; }
 
 // Workspace: [split counters | (m, l) partials | O partials].  The counter
 // region has a FIXED size at offset 0 so that no call's partials ever overlap

@@ -332,7 +332,7 @@ int env_int(const char* name, int dflt);
 int head_subgroup(int gqa);                         // query heads per workgroup
 int plan_chunk(int max_len, int64_t groups, int min_splits);        // keys per workgroup
 int max_splits_bound(int max_len, int64_t groups, int min_splits);  // bound of ceil(L / chunk)
-int min_splits_for(int batch);                                      // 8 for batched launches
+int min_splits_for(int batch);                                      // 5 for batched launches
 WsLayout ws_layout(int batch, int Hq, int D, int max_splits);
 
 // Launch of the matrix-core kernel (tq_sdpa_mfma.hip).  Returns TQ_OK,
