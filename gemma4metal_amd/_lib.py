@@ -95,11 +95,16 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> int:
-    lib = load()
-    st = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    st = fn(*args)
     if st != 0:
-        raise TQError(name, st, lib.tq_last_error().decode())
+        raise TQError(name, st, load().tq_last_error().decode())
     return st
 
 

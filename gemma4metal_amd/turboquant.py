@@ -12,6 +12,7 @@ buffer grown on demand and reused (the kernels leave it zeroed).
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Optional
 
 import torch
@@ -26,14 +27,22 @@ _MODES = {"mlx": TQ_QUANT_MLX, "minmax": TQ_QUANT_MINMAX}
 _workspaces: dict = {}
 
 
+# Pointer and stream arguments are passed as plain ints (or None for NULL):
+# the C-ABI argtypes convert them, and a decode call's fixed host cost is
+# part of a short layer's time.
 def _ptr(t: Optional[torch.Tensor]):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    return t.data_ptr() if t is not None else None
 
 
-def _stream(stream) -> ctypes.c_void_p:
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(stream) -> int:
     if stream is None:
+        if _raw_stream is not None:
+            return _raw_stream(torch.cuda.current_device())
         stream = torch.cuda.current_stream()
-    return ctypes.c_void_p(stream.cuda_stream)
+    return stream.cuda_stream
 
 
 def _need(cond: bool, msg: str):
@@ -86,29 +95,41 @@ def sdpa_int4(queries: torch.Tensor,
                  ("v_biases", v_biases)):
         _check_cuda(n, t)
     _need(queries.dim() == 2, "queries must be (num_heads, head_dim)")
-    _need(queries.dtype in _DT, "queries must be float32, float16 or bfloat16")
+    qdt = _DT.get(queries.dtype)
+    _need(qdt is not None, "queries must be float32, float16 or bfloat16")
     Hq, D = queries.shape
     _need(k_quant.dim() == 3 and k_quant.dtype in _QUANT_DT, "k_quant must be (Hkv, N, D/8) uint32")
-    Hkv, cap, _ = k_quant.shape
-    for n, t in (("k_quant", k_quant), ("v_quant", v_quant)):
-        _need(t.shape == (Hkv, cap, D // 8) and t.dtype in _QUANT_DT, f"{n} must be ({Hkv}, {cap}, {D // 8}) uint32")
+    qshape = k_quant.shape
+    Hkv, cap = qshape[0], qshape[1]
+    _need(qshape[2] == D // 8, f"k_quant must be ({Hkv}, {cap}, {D // 8}) uint32")
+    _need(v_quant.shape == qshape and v_quant.dtype in _QUANT_DT, f"v_quant must be ({Hkv}, {cap}, {D // 8}) uint32")
     sbt = _sb_dtype("k_scales", k_scales)
+    sshape = (Hkv, cap, D // 64)
+    sdt = k_scales.dtype
     for n, t in (("k_scales", k_scales), ("k_biases", k_biases), ("v_scales", v_scales),
                  ("v_biases", v_biases)):
-        _need(t.shape == (Hkv, cap, D // 64), f"{n} must be ({Hkv}, {cap}, {D // 64})")
-        _need(_DT.get(t.dtype) == sbt, "scales and biases must share one dtype")
+        _need(t.shape == sshape, f"{n} must be ({Hkv}, {cap}, {D // 64})")
+        _need(t.dtype == sdt, "scales and biases must share one dtype")
     n = cap if kv_len is None else int(kv_len)
     if out is None:
         out = torch.empty((Hq, D), dtype=torch.float32, device=queries.device)
-    _check_cuda("out", out)
-    _need(out.shape == (Hq, D) and out.dtype == torch.float32, "out must be (Hq, D) float32")
-    nbytes = _lib.load().tq_sdpa_int4_workspace_size(1, Hq, Hkv, D, n)
+    else:
+        _check_cuda("out", out)
+        _need(out.shape == (Hq, D) and out.dtype == torch.float32, "out must be (Hq, D) float32")
+    nbytes = _decode_ws_size(Hq, Hkv, D, n)
     ws = workspace(nbytes, queries.device)
-    call("tq_sdpa_int4", _ptr(queries), _DT[queries.dtype], _ptr(k_quant), _ptr(k_scales),
-         _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out),
-         Hq, Hkv, D, n, cap, int(gqa_factor), float(scale), int(sliding_window), _ptr(ws),
-         ws.numel(), _stream(stream))
+    call("tq_sdpa_int4", queries.data_ptr(), qdt, k_quant.data_ptr(), k_scales.data_ptr(),
+         k_biases.data_ptr(), v_quant.data_ptr(), v_scales.data_ptr(), v_biases.data_ptr(), sbt,
+         out.data_ptr(), Hq, Hkv, D, n, cap, int(gqa_factor), float(scale), int(sliding_window),
+         ws.data_ptr(), ws.numel(), _stream(stream))
     return out
+
+
+@functools.lru_cache(maxsize=256)
+def _decode_ws_size(Hq: int, Hkv: int, D: int, n: int) -> int:
+    """Workspace bytes of one single-sequence decode call (a pure function
+    of the shape, cached: the C query costs a call per layer otherwise)."""
+    return _lib.load().tq_sdpa_int4_workspace_size(1, Hq, Hkv, D, n)
 
 
 def sdpa_int4_prefill(queries: torch.Tensor,
