@@ -694,18 +694,21 @@ struct P7Keys {
 //     with code kp whose child pairs have codes k0, k1:
 //     (cos_p cos_0, cos_p sin_0, sin_p cos_1, sin_p sin_1) -- two levels of
 //     the top-down decode per lookup (levels 7-6, 5-4, 3-2).
+// The G heads' entries of t1 and tq are adjacent, so one 8-byte LDS read
+// (G = 2) serves both heads of a lookup.
 template <int G>
 struct P7Tables {
-  float t1[G][64][16];  // rows rotated, see p7_t1_row
-  float tq[G][16][256];
+  float t1[64][16][G];  // [row (rotated, see p7_t1_row)][codeword][head]
+  float tq[16][256][G];  // [QJL byte position][byte value][head]
   float4 t2[64];
   float U[G];
 };
 
 // LDS row of level-1 row 16 qt + jj (pair jj of quarter qt): the rows are
 // rotated within each group of four, to 16 qt + (jj & ~3) + ((jj + qt) & 3).
-// The four lanes of a key read row jj of their quarters in one instruction;
-// the rotation puts those rows into four different 16-bank groups.
+// The four lanes of a key read row jj of their quarters in one instruction.
+// At G = 1 (64 B rows) the rotation puts those rows into four different
+// 16-bank groups; at G = 2 a row covers all banks and it changes nothing.
 __device__ __forceinline__ int p7_t1_row(int row) {
   const int qt = row >> 4, jj = row & 15;
   return (row & ~15) | (jj & ~3) | ((jj + qt) & 3);
@@ -723,8 +726,16 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
   for (int i = threadIdx.x; i < G * kVec; i += NT) {
     const int g = i / kVec, r = i - (i / kVec) * kVec;
     const float4 v = reinterpret_cast<const float4*>(k.qtab + static_cast<int64_t>(h0 + g) * kP7QTab)[r];
-    if (r < 256) reinterpret_cast<float4*>(&T.t1[g][0][0])[p7_t1_row(r >> 2) * 4 + (r & 3)] = v;
-    else if (r < 1280) reinterpret_cast<float4*>(&T.tq[g][0][0])[r - 256] = v;
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    if (r < 256) {
+      const int row = p7_t1_row(r >> 2), c0 = 4 * (r & 3);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) T.t1[row][c0 + k][g] = f[k];
+    } else if (r < 1280) {
+      const int e = 4 * (r - 256), pos = e >> 8, b0 = e & 255;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) T.tq[pos][b0 + k][g] = f[k];
+    }
     else if (r == 1280) T.U[g] = (v.x + v.y) + (v.z + v.w);
   }
   if (threadIdx.x < 64) {
@@ -996,23 +1007,24 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
   }
   // byte addresses: lane base + (index << 2), constant parts in the
   // instruction's offset field
-  const char* tqb = reinterpret_cast<const char*>(&T.tq[0][0][0]) + qt * 4096;
+  constexpr int kE = 4 * G;  // bytes of one table entry (G heads)
+  const char* tqb = reinterpret_cast<const char*>(&T.tq[0][0][0]) + qt * (4 * 256 * kE);
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     const uint32_t byte = __builtin_amdgcn_ubfe(Q.qj, 8 * b, 8);
+    const float* e = reinterpret_cast<const float*>(tqb + b * (256 * kE) + byte * kE);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-      qa[g] += *reinterpret_cast<const float*>(tqb + g * 16384 + b * 1024 + (byte << 2));
+    for (int g = 0; g < G; ++g) qa[g] += e[g];
   }
   const float R = h2f_lo(Q.nrm), rn = h2f_hi(Q.nrm);
   const float r5 = R * pick4(ta, qt);
   const float r3[4] = {r5 * tb.x, r5 * tb.y, r5 * tb.z, r5 * tb.w};
   // rotated level-1 rows (p7_t1_row): row jj of quarter qt is at
   // 16 qt + (jj & ~3) + ((jj + qt) & 3)
-  const char* t1b = reinterpret_cast<const char*>(&T.t1[0][0][0]) + qt * 1024;
+  const char* t1b = reinterpret_cast<const char*>(&T.t1[0][0][0]) + qt * (16 * 16 * kE);
   uint32_t rot[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) rot[e] = static_cast<uint32_t>((e + qt) & 3) * 64;
+  for (int e = 0; e < 4; ++e) rot[e] = static_cast<uint32_t>((e + qt) & 3) * (16 * kE);
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
     const float r1[4] = {r3[ii] * tc[ii].x, r3[ii] * tc[ii].y, r3[ii] * tc[ii].z, r3[ii] * tc[ii].w};
@@ -1021,10 +1033,9 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
     for (int e = 0; e < 4; ++e) {
       const int jj = 4 * ii + e;  // level-1 pair 16 qt + jj
       const uint32_t nib = __builtin_amdgcn_ubfe(word, 4 * (jj % 8), 4);
-      const char* row = t1b + ii * 256 + rot[e] + (nib << 2);
+      const float* ent = reinterpret_cast<const float*>(t1b + ii * (4 * 16 * kE) + rot[e] + nib * kE);
 #pragma unroll
-      for (int g = 0; g < G; ++g)
-        acc[g] = fmaf(r1[e], *reinterpret_cast<const float*>(row + g * 4096), acc[g]);
+      for (int g = 0; g < G; ++g) acc[g] = fmaf(r1[e], ent[g], acc[g]);
     }
   }
   const float cr = kQjlCoef * rn;
