@@ -98,6 +98,14 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// The same butterfly as a max over aligned groups of 16 lanes.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+}
+
 // The same butterfly over all 64 lanes for a max, and for an exact int32
 // sum: four DPP steps inside each row of 16 lanes, then two cross-row
 // shuffles.

@@ -870,20 +870,14 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(SdpaParams p, int D) 
     }
     M = Mn;
   }
-  float Mall = M;
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) Mall = fmaxf(Mall, shfl_xor_f(Mall, off));
+  // the 16 lanes of an output: DPP butterflies within the row
+  const float Mall = row16_max(M);
   const float f = merge_factor(M, Mall);
-  L *= f;
-  O.x *= f; O.y *= f; O.z *= f; O.w *= f;
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) {
-    O.x += shfl_xor_f(O.x, off);
-    O.y += shfl_xor_f(O.y, off);
-    O.z += shfl_xor_f(O.z, off);
-    O.w += shfl_xor_f(O.w, off);
-    L += shfl_xor_f(L, off);
-  }
+  L = group_sum<16>(L * f);
+  O.x = group_sum<16>(O.x * f);
+  O.y = group_sum<16>(O.y * f);
+  O.z = group_sum<16>(O.z * f);
+  O.w = group_sum<16>(O.w * f);
   if (sl == 0) {
     float* out = p.out + head * D + 4 * d4;
     out[0] = normalise(O.x, L, p.denom_eps);
