@@ -77,11 +77,40 @@ __device__ __forceinline__ uint32_t shfl_xor_u(uint32_t v, int off) {
   return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64));
 }
 
+// v combined with its value in lane l ^ 16 or l ^ 32, in VALU: gfx950's
+// v_permlane16_swap / v_permlane32_swap of v with itself leave the pair
+// {v[l], v[l ^ 16]} (resp. {v[l], v[l ^ 32]}) in the two results of every
+// lane (lane layout checked on hardware), with no LDS round trip.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int xor16_sum(int v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  return static_cast<int>(r[0] + r[1]);
+}
+__device__ __forceinline__ int xor32_sum(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  return static_cast<int>(r[0] + r[1]);
+}
+
 // Butterfly sum over aligned groups of N consecutive lanes (N <= 64), every
 // lane of the group receiving the total.  Within a row of 16 lanes this uses
 // DPP (quad_perm xor-1 / xor-2, half-row mirror, row mirror), which is exact
 // for a butterfly because after the first two steps all lanes of a quad hold
-// the same value; beyond 16 lanes it falls back to ds_bpermute.
+// the same value; beyond 16 lanes it uses the permlane swaps above.
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "N");
@@ -93,8 +122,8 @@ __device__ __forceinline__ float group_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
   if constexpr (N >= 16)
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
-  if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
-  if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (N >= 32) v = xor16_sum(v);
+  if constexpr (N >= 64) v = xor32_sum(v);
   return v;
 }
 
@@ -107,23 +136,21 @@ __device__ __forceinline__ float row16_max(float v) {
 }
 
 // The same butterfly over all 64 lanes for a max, and for an exact int32
-// sum: four DPP steps inside each row of 16 lanes, then two cross-row
-// shuffles.
+// sum: four DPP steps inside each row of 16 lanes, then the two cross-row
+// permlane swaps.
 __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  return xor32_max(xor16_max(v));
 }
 __device__ __forceinline__ int wave_sum_dpp(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
   v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  return xor32_sum(xor16_sum(v));
 }
 
 // exp2 with -inf handled (v_exp_f32 returns 0 for -inf already; kept explicit).

@@ -116,16 +116,8 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, shfl_xor_f(v, off));
-  return v;
-}
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) v += shfl_xor_f(v, off);
-  return v;
-}
+__device__ __forceinline__ float wave_max_f(float v) { return wave_max_dpp(v); }
+__device__ __forceinline__ float wave_sum_f(float v) { return group_sum<64>(v); }
 
 // ============================================================================
 // Reference layouts: 16-value blocks, 4 levels
@@ -1308,10 +1300,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // columns: sum the four K-slot groups; lane (vm, vc) holds V words
   // 4 vc + i (dims 8 (4 vc + i) + 2 byte + half) of column vm, and the words
   // of quant group cgr are those with vc >> 1 == cgr
-  wsum += shfl_xor_f(wsum, 16);
-  wsum += shfl_xor_f(wsum, 32);
-  bacc += shfl_xor_f(bacc, 16);
-  bacc += shfl_xor_f(bacc, 32);
+  wsum = xor16_sum(wsum);
+  wsum = xor32_sum(wsum);
+  bacc = xor16_sum(bacc);
+  bacc = xor32_sum(bacc);
   float ls[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) ls[g] = wave_sum_f(l_run[g]);

@@ -234,8 +234,8 @@ void prefill_int4_kernel(SdpaParams p) {
     float mt = sc[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    mt = xor16_max(mt);
+    mt = xor32_max(mt);
     const float m_new = fmaxf(m_run, mt);
     if (it == 0) {
       m_run = m_new;  // first tile: nothing accumulated yet
@@ -282,8 +282,8 @@ void prefill_int4_kernel(SdpaParams p) {
   }
 
   // ---- normalise and store row m: dims 16 b + 4c + i -------------------------
-  float l_sum = l_run + shfl_xor_f(l_run, 16);
-  l_sum += shfl_xor_f(l_sum, 32);
+  float l_sum = xor16_sum(l_run);
+  l_sum = xor32_sum(l_sum);
   if (row_ok) {
     float* out = p.out + qrow * D;
 #pragma unroll
@@ -421,8 +421,8 @@ void prefill_int4_ws_kernel(SdpaParams p) {
     float mt = sc[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    mt = xor16_max(mt);
+    mt = xor32_max(mt);
     const float m_new = fmaxf(m_run, mt);
     if (it == 0) {
       m_run = m_new;  // first tile: nothing accumulated yet
@@ -468,8 +468,8 @@ void prefill_int4_ws_kernel(SdpaParams p) {
   }
 
   // ---- normalise and store row m: dims 16 b + 4c + i -------------------------
-  float l_sum = l_run + shfl_xor_f(l_run, 16);
-  l_sum += shfl_xor_f(l_sum, 32);
+  float l_sum = xor16_sum(l_run);
+  l_sum = xor32_sum(l_sum);
   if (row_ok) {
     float* out = p.out + qrow * D;
 #pragma unroll

@@ -351,8 +351,8 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     // online softmax over the 32 keys, per head (column)
     float mt = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                      fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    mt = xor16_max(mt);
+    mt = xor32_max(mt);
     const float m_new = fmaxf(m_run, mt);
     if (t0 == base0) {
       m_run = m_new;  // first batch: nothing accumulated yet
@@ -438,14 +438,14 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   // ---- per-wave result into the finalisation arena --------------------------
   // lane (m, c) holds V words 16 blk + 4c + i of column m; the column's
   // group in block blk is 2 blk + m / 8, the words' group 2 blk + c / 2
-  float l_sum = l_run + shfl_xor_f(l_run, 16);
-  l_sum += shfl_xor_f(l_sum, 32);
+  float l_sum = xor16_sum(l_run);
+  l_sum = xor32_sum(l_sum);
 #pragma unroll
   for (int blk = 0; blk < 4; ++blk) {
-    wsum[blk] += shfl_xor_f(wsum[blk], 16);
-    wsum[blk] += shfl_xor_f(wsum[blk], 32);
-    bacc[blk] += shfl_xor_f(bacc[blk], 16);
-    bacc[blk] += shfl_xor_f(bacc[blk], 32);
+    wsum[blk] = xor16_sum(wsum[blk]);
+    wsum[blk] = xor32_sum(wsum[blk]);
+    bacc[blk] = xor16_sum(bacc[blk]);
+    bacc[blk] = xor32_sum(bacc[blk]);
   }
   if ((c >> 1) == (m >> 3)) {
     float* o = Fin::o(arena, wave, hh);
@@ -646,8 +646,8 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       // online softmax (lazy rescale); the factor goes to the consumer
       float mt = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
                        fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-      mt = fmaxf(mt, shfl_xor_f(mt, 16));
-      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      mt = xor16_max(mt);
+      mt = xor32_max(mt);
       const float m_new = fmaxf(m_run, mt);
       float f = 1.0f;
       if (st == 0) {
@@ -715,14 +715,14 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 
     // per-column results: (m, l) into the arena (the operand slots are dead
     // now), the offsets of the weight sums for the consumers
-    float l_sum = l_run + shfl_xor_f(l_run, 16);
-    l_sum += shfl_xor_f(l_sum, 32);
+    float l_sum = xor16_sum(l_run);
+    l_sum = xor32_sum(l_sum);
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
-      wsum[blk] += shfl_xor_f(wsum[blk], 16);
-      wsum[blk] += shfl_xor_f(wsum[blk], 32);
-      bacc[blk] += shfl_xor_f(bacc[blk], 16);
-      bacc[blk] += shfl_xor_f(bacc[blk], 32);
+      wsum[blk] = xor16_sum(wsum[blk]);
+      wsum[blk] = xor32_sum(wsum[blk]);
+      bacc[blk] = xor16_sum(bacc[blk]);
+      bacc[blk] = xor32_sum(bacc[blk]);
       if (c == 0) off_lds[s][blk][m] = bacc[blk] - 128.0f * wsum[blk];
     }
     if (c == 0 && m < 8) {

@@ -394,8 +394,8 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     float mt = sc[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
-    mt = fmaxf(mt, shfl_xor_f(mt, 16));
-    mt = fmaxf(mt, shfl_xor_f(mt, 32));
+    mt = xor16_max(mt);
+    mt = xor32_max(mt);
     const float m_new = fmaxf(m_run, mt);
     if (t0 == base0) {
       m_run = m_new;  // first batch: nothing accumulated yet
@@ -493,12 +493,12 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // The V MFMAs contract over the keys of all four lane groups, so the
   // per-lane sums (softmax denominator, weight sum of the 128 offset, bias
   // term) are totalled over the lane groups of the same column.
-  float l_sum = l_run + shfl_xor_f(l_run, 16);
-  l_sum += shfl_xor_f(l_sum, 32);
-  wsum += shfl_xor_f(wsum, 16);
-  wsum += shfl_xor_f(wsum, 32);
-  bacc += shfl_xor_f(bacc, 16);
-  bacc += shfl_xor_f(bacc, 32);
+  float l_sum = xor16_sum(l_run);
+  l_sum = xor32_sum(l_sum);
+  wsum = xor16_sum(wsum);
+  wsum = xor32_sum(wsum);
+  bacc = xor16_sum(bacc);
+  bacc = xor32_sum(bacc);
   if (col_used) {
     // a wave's arena slot covers every dim: its own V words' dims get the
     // result, the other V half's dims zero; only V half 0 counts the
