@@ -794,7 +794,7 @@ __global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, con
   } else {
     acc = half == 0 ? xs[i] : 0.0f;
   }
-  acc += shfl_xor_f(acc, 1);
+  acc = group_sum<2>(acc);
   if (half == 0) {
     qp[i] = acc;
     if (q_rot && part == 0) q_rot[static_cast<int64_t>(h) * 128 + i] = acc;
@@ -810,7 +810,7 @@ __global__ __launch_bounds__(256) void polar7_prepare_kernel(const float* q, con
     us = fmaf(x[2], a.z, us);
     us = fmaf(x[3], a.w, us);
   }
-  us += shfl_xor_f(us, 1);
+  us = group_sum<2>(us);
   if (half == 0) {
     u[i] = us;
     if (q_sketch && part == 0) q_sketch[static_cast<int64_t>(h) * 128 + i] = us;
@@ -900,8 +900,7 @@ __global__ __launch_bounds__(256) void polar7_prepare_sp_kernel(const float* q, 
     acc = fmaf(x[3], a.w, acc);
   }
   if (o < 32 && !P) acc = qr == 0 ? xs[r0 + o] : 0.0f;
-  acc += shfl_xor_f(acc, 1);
-  acc += shfl_xor_f(acc, 2);
+  acc = group_sum<4>(acc);
   if (qr == 0) {
     const int r = r0 + (o & 31);
     if (o < 32) {
@@ -1040,8 +1039,7 @@ template <int G>
 __device__ __forceinline__ void quarter_sum(float s[G]) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    s[g] += shfl_xor_f(s[g], 1);
-    s[g] += shfl_xor_f(s[g], 2);
+    s[g] = group_sum<4>(s[g]);  // DPP quad permutes: (a + b) + (c + d)
   }
 }
 
