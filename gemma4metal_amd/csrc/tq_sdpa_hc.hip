@@ -231,15 +231,18 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   const int safe_last = max(last, 0);
 
   // q first (one dword per element, no branch around the load), then the
-  // first iteration's K/V, which stay in flight through the prologue
+  // first iteration's K/V, which stay in flight through the prologue.  A
+  // 16-bit element's half of its dword depends on the element's index only
+  // (kNT is even), and is selected at conversion: shifting right after the
+  // load would wait for q before the K/V loads go out.
   uint32_t qraw[NE];
   const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
   const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+  const uint32_t qsh = qsz == 2 && ((qbase + threadIdx.x) & 1) ? 16u : 0u;
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
     const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
     qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-    if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
   }
   __builtin_amdgcn_sched_barrier(0);
   HcBuf bufA, bufB;
@@ -253,7 +256,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   float qv[NE];
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
-    const uint32_t w = qraw[k];
+    const uint32_t w = qraw[k] >> qsh;
     const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
                     : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
                                           : __uint_as_float(w << 16);
@@ -539,21 +542,24 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   const int safe_last = max(last, 0);
   auto tclamp = [&](int t0) { return min(t0, safe_last); };
 
+  // q: one dword per element; a 16-bit element's half of its dword depends
+  // on the element's index only (kNT is even) and is selected at conversion,
+  // so the K/V loads issued after q do not wait for it
+  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
+  const uint32_t qsh = qsz == 2 && ((qbase + threadIdx.x) & 1) ? 16u : 0u;
   auto load_q = [&](uint32_t (&qraw)[NE]) {
-    const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
-    const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
       const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
       qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-      if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
     }
   };
   auto q_image = [&](const uint32_t (&qraw)[NE]) {
     float qv[NE];
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
-      const uint32_t w = qraw[k];
+      const uint32_t w = qraw[k] >> qsh;
       const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
                       : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
                                             : __uint_as_float(w << 16);

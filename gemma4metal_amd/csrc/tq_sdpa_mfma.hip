@@ -229,7 +229,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // (one dword load per element for every q dtype -- no branch around the
   // load, so the wait before the prologue covers q only, not the K/V loads
   // issued after it)
-  uint32_t qraw[NE];
+  uint32_t qraw[NE], qsh[NE];  // dword of each element, and its 16-bit half
   const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
@@ -240,7 +240,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     const int64_t qrow = static_cast<int64_t>(min(b0 + v / GH, b_last)) * p.Hq + h0 + v % GH;
     const int64_t byte = (qrow * D + (e - v * D)) * qsz;
     qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-    if (qsz == 2 && (byte & 2)) qraw[k] >>= 16;
+    qsh[k] = qsz == 2 && (byte & 2) ? 16u : 0u;  // applied at conversion, not here
   }
   __builtin_amdgcn_sched_barrier(0);
   // Issued unconditionally (a load under a branch makes the compiler drain
@@ -257,7 +257,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   float qv[NE];
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
-    const uint32_t w = qraw[k];
+    const uint32_t w = qraw[k] >> qsh[k];
     const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
                     : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
                                           : __uint_as_float(w << 16);
