@@ -973,10 +973,6 @@ __device__ __forceinline__ void load_p7_quarter(const P7Rows& R, uint32_t off, i
   Q.nrm = nt_at<uint32_t>(R.nrm, off * 4);
 }
 
-__device__ __forceinline__ float pick4(const float4& v, int i) {
-  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
 // Quarter qt's part of the score of one key for the G heads of the tables;
 // the four quarters (lanes 4m .. 4m+3) sum to
 // sc * (sum_j r1_j t1[j][n_j] + coef ||r|| (2 sum tq - U)).
@@ -984,7 +980,8 @@ template <int G>
 __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Quarter& Q, int qt,
                                                  float sc, float out[G]) {
   const uint32_t w11 = Q.w11, w10 = Q.w10;
-  const float4 ta = T.t2[((w11 >> 28) & 3u) | ((w11 >> 22) & 0x3Cu)];
+  // the top pair's factor: one float of the entry per quarter lane
+  const float ta_q = reinterpret_cast<const float*>(&T.t2[((w11 >> 28) & 3u) | ((w11 >> 22) & 0x3Cu)])[qt];
   const float4 tb = T.t2[((w11 >> (16 + 2 * qt)) & 3u) | (((w11 >> (4 * qt)) & 15u) << 2)];
   float4 tc[4];
 #pragma unroll
@@ -1008,7 +1005,7 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
     for (int g = 0; g < G; ++g) qa[g] += e[g];
   }
   const float R = h2f_lo(Q.nrm), rn = h2f_hi(Q.nrm);
-  const float r5 = R * pick4(ta, qt);
+  const float r5 = R * ta_q;
   const float r3[4] = {r5 * tb.x, r5 * tb.y, r5 * tb.z, r5 * tb.w};
   // rotated level-1 rows (p7_t1_row): row jj of quarter qt is at
   // 16 qt + (jj & ~3) + ((jj + qt) & 3)
