@@ -1041,13 +1041,13 @@ __device__ __forceinline__ void quarter_sum(float s[G]) {
 }
 
 // Scores only (compressed_score over polar7 keys): four lanes per key, NT / 4
-// keys per pass of an NT-thread workgroup, 16 passes per workgroup; the next
+// keys per pass of an NT-thread workgroup, NP passes per workgroup; the next
 // pass's words are loaded while the current pass is scored.  Grid (key
 // blocks, kv heads * head subgroups).
-template <int G, int NT>
+template <int G, int NT, int NP>
 __global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int cap, int gqa,
                                                           int n_sub, float scale) {
-  constexpr int KPP = NT / 4, KPW = 16 * KPP;  // keys per pass, per workgroup
+  constexpr int KPP = NT / 4, KPW = NP * KPP;  // keys per pass, per workgroup
   __shared__ P7Tables<G> T;
   const int hy = blockIdx.y, kvh = hy / n_sub, sub = hy - (hy / n_sub) * n_sub;
   const int h0 = kvh * gqa + sub * G;
@@ -1055,7 +1055,7 @@ __global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int c
   const int t0 = blockIdx.x * KPW + key;
   const int last = n - 1;
   const int64_t rowbase = static_cast<int64_t>(kvh) * cap;
-  const int npass = min(16, (n - blockIdx.x * KPW + KPP - 1) / KPP);
+  const int npass = min(NP, (n - blockIdx.x * KPW + KPP - 1) / KPP);
   // rows of this workgroup: rowbase + blockIdx.x * KPW + (0 .. lim)
   const P7Rows R = p7_rows(k, rowbase + blockIdx.x * KPW);
   const uint32_t lim = static_cast<uint32_t>(last - blockIdx.x * KPW);
@@ -1799,13 +1799,13 @@ int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_
   k.scores = scores;
   const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, kP7MaxG), n_sub = gqa / G;
   TQ_CHECK_ARG(num_kv_heads * n_sub <= 65535, "%s: too many heads", fn);
-  // 512 threads (two waves per SIMD), 2048 keys per workgroup: the staged
-  // query tables are paid once per 2048 keys
-  constexpr int NT = 512, KPW = 16 * NT / 4;
+  // 1024 threads (four waves per SIMD) in 8 passes, 2048 keys per workgroup:
+  // the staged query tables are paid once per 2048 keys
+  constexpr int NT = 1024, NP = 8, KPW = NP * NT / 4;
   dim3 grid((kv_len + KPW - 1) / KPW, num_kv_heads * n_sub);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (G == 1) polar7_score_kernel<1, NT><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
-  else polar7_score_kernel<2, NT><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  if (G == 1) polar7_score_kernel<1, NT, NP><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  else polar7_score_kernel<2, NT, NP><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
   TQ_CHECK_LAUNCH("polar7_score_kernel");
   return TQ_OK;
 }
