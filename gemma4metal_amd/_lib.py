@@ -37,7 +37,10 @@ SIGNATURES = {
     "tq_memset": (I, [P, I, SZ]),
     "tq_sync": (I, []),
     "tq_stream_read": (I, [P, SZ, P, I, P]),
+    "tq_stream_read_tiles": (I, [P, SZ, P, I, I, I, I, I, P]),
     "tq_sdpa_int4_workspace_size": (SZ, [I, I, I, I, I]),
+    "tq_sdpa_int4_plan": (I, [I, I, I, I, I, I, I, I, P, P, P, SZ]),
+    "tq_reload_options": (I, []),
     "tq_sdpa_int4": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, I, F, I, P, SZ, P]),
     "tq_sdpa_int4_ragged": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, P, P, I, I, F, I,
                                 P, SZ, P]),

@@ -483,14 +483,17 @@ void prefill_int4_ws_kernel(SdpaParams p) {
 
 // Returns -1 when the tile kernel does not serve the shape (the caller then
 // runs the split-K decode kernels in prefill mode).
+bool prefill_tiles_serve(int D, int sb_dtype, int gqa) {
+  if (sb_dtype != TQ_F16 || (D != 128 && D != 256 && D != 512)) return false;
+  return gqa >= 1 && gqa <= kPfRows && kPfRows % gqa == 0;
+}
+
 int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t s) {
-  if (sb_dtype != TQ_F16 || (D != 128 && D != 256 && D != 512)) return -1;
-  if (p.gqa < 1 || p.gqa > kPfRows || kPfRows % p.gqa != 0) return -1;
+  if (!prefill_tiles_serve(D, sb_dtype, p.gqa)) return -1;
   const int qpw = kPfRows / p.gqa;
   dim3 grid((p.nq + qpw - 1) / qpw, p.Hkv);
-  // TQ_PREFILL_WS=0 selects the one-role kernel at D 128 / 256 (read per call)
-  const char* wsv = std::getenv("TQ_PREFILL_WS");
-  const bool ws = !(wsv && wsv[0] == '0');
+  // TQ_PREFILL_WS=0 selects the one-role kernel at D 128 / 256
+  const bool ws = options().prefill_ws;
   if (D == 128 && ws) prefill_int4_ws_kernel<128><<<grid, 2 * kPfThreads, 0, s>>>(p);
   else if (D == 256 && ws) prefill_int4_ws_kernel<256><<<grid, 2 * kPfThreads, 0, s>>>(p);
   else if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);

@@ -32,7 +32,10 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "tq_sdpa_common.h"
@@ -61,9 +64,39 @@ constexpr int kMinChunk = 128;
 constexpr int kChunkGranule = 128;
 }  // namespace
 
-int env_int(const char* name, int dflt) {
-  const char* v = std::getenv(name);
-  return v ? std::atoi(v) : dflt;
+namespace {
+// The switches of Options, as atomics so that a reload while other threads
+// plan calls is well defined (each call sees old or new values).
+struct OptionStore {
+  std::atomic<int> sdpa_valu{0}, sdpa_chunk{0}, prefill_splitk{0}, prefill_ws{1}, hc_one{0};
+};
+OptionStore g_opts;
+std::once_flag g_opts_once;
+
+void read_options() {
+  auto env = [](const char* name) -> const char* { return std::getenv(name); };
+  const char* v = env("TQ_SDPA_IMPL");
+  g_opts.sdpa_valu.store(v && std::string(v) == "valu", std::memory_order_relaxed);
+  v = env("TQ_SDPA_CHUNK");
+  g_opts.sdpa_chunk.store(v ? std::atoi(v) : 0, std::memory_order_relaxed);
+  v = env("TQ_PREFILL_IMPL");
+  g_opts.prefill_splitk.store(v && std::string(v) == "splitk", std::memory_order_relaxed);
+  v = env("TQ_PREFILL_WS");
+  g_opts.prefill_ws.store(!(v && v[0] == '0'), std::memory_order_relaxed);
+  v = env("TQ_HC_IMPL");
+  g_opts.hc_one.store(v && v[0] == '1', std::memory_order_relaxed);
+}
+}  // namespace
+
+Options options() {
+  std::call_once(g_opts_once, read_options);
+  Options o;
+  o.sdpa_valu = g_opts.sdpa_valu.load(std::memory_order_relaxed) != 0;
+  o.sdpa_chunk = g_opts.sdpa_chunk.load(std::memory_order_relaxed);
+  o.prefill_splitk = g_opts.prefill_splitk.load(std::memory_order_relaxed) != 0;
+  o.prefill_ws = g_opts.prefill_ws.load(std::memory_order_relaxed) != 0;
+  o.hc_one = g_opts.hc_one.load(std::memory_order_relaxed) != 0;
+  return o;
 }
 
 int head_subgroup(int gqa) {
@@ -82,7 +115,7 @@ int head_subgroup(int gqa) {
 int plan_chunk(int max_len, int64_t groups, int min_splits) {
   // never more than kMaxSplits chunks per sequence
   const int64_t floor_c = (static_cast<int64_t>(max_len) + kMaxSplits - 1) / kMaxSplits;
-  const int forced = env_int("TQ_SDPA_CHUNK", 0);
+  const int forced = options().sdpa_chunk;
   if (forced > 0) return static_cast<int>(std::max<int64_t>(forced, floor_c));
   const int64_t want = (static_cast<int64_t>(max_len) * groups + target_wgs() - 1) / target_wgs();
   int64_t c = (want + kChunkGranule - 1) / kChunkGranule * kChunkGranule;
@@ -99,7 +132,7 @@ int plan_chunk(int max_len, int64_t groups, int min_splits) {
 // and workspaces.
 int max_splits_bound(int max_len, int64_t groups, int min_splits) {
   if (max_len <= 0) return 1;
-  const int forced = env_int("TQ_SDPA_CHUNK", 0);
+  const int forced = options().sdpa_chunk;
   if (forced > 0) return std::min((max_len + forced - 1) / forced, kMaxSplits);  // chunk >= ceil(L/kMaxSplits)
   const int64_t by_len = (static_cast<int64_t>(max_len) + kMinChunk - 1) / kMinChunk;
   const int64_t by_wgs = std::max<int64_t>((target_wgs() + groups - 1) / groups, min_splits);
@@ -121,6 +154,77 @@ WsLayout ws_layout(int batch, int Hq, int D, int max_splits) {
   w.o_off = w.ml_off + up(sizeof(float) * 2 * static_cast<size_t>(batch) * Hq * max_splits);
   w.total = w.o_off + up(sizeof(float) * static_cast<size_t>(batch) * Hq * max_splits * D);
   return w;
+}
+
+// Kernel choice and split plan of a call (validated arguments).
+// - D = 512 with GQA a multiple of 8: the heads-as-columns kernel (8 heads
+//   per workgroup, each K/V byte unpacked once), merged by a separate
+//   kernel.
+// - Otherwise the matrix-core kernel where it serves (D, G); at D = 512 it
+//   takes at most 2 query heads per workgroup (2 heads x 8 quant groups
+//   fill its 16 columns): the head subgroups of one kv head then read the
+//   same K/V, concurrently and on one XCD, so the repeats are served mostly
+//   from L2.  (The workspace bound of tq_sdpa_int4_workspace_size, planned
+//   with the largest subgroup, covers this: more groups never means more
+//   splits.)
+// - Prefill of >= 64 queries: the K/V-tile kernels where they serve.
+// - The VALU kernel under TQ_SDPA_IMPL=valu.
+SdpaPlan plan_sdpa(int mode, int batch, int Hq, int Hkv, int D, int max_len, int gqa, int window,
+                   int sb_dtype) {
+  (void)Hq;
+  const Options o = options();
+  const bool prefill = mode == 2;
+  const bool try_mfma = !o.sdpa_valu;
+  SdpaPlan pl{};
+  const bool hc = try_mfma && D == 512 && gqa % 8 == 0 && hc_serves(sb_dtype);
+  int G = head_subgroup(gqa);
+  // the matrix-core kernel takes at most 16 (head, quant group) columns:
+  // halve the head subgroup until it serves the shape
+  if (try_mfma && !hc)
+    while (G > 1 && !mfma_serves(D, G, sb_dtype)) G /= 2;
+  pl.G = G;
+  pl.n_sub = gqa / G;
+  const int64_t groups = static_cast<int64_t>(batch) * Hkv * pl.n_sub;
+  // Prefill on the matrix-core kernel: pq consecutive queries share a
+  // workgroup (its G * pq column sets fill the 16 MFMA columns), so each K/V
+  // byte serves pq queries.  Split planning stays per query, and a group's
+  // key range is the union of its windows (at most window + pq - 1 keys).
+  int pq = 1;
+  if (prefill && try_mfma && !hc && mfma_serves(D, G, sb_dtype)) {
+    const int max_cols = D == 128 ? 8 : (D == 256 ? 4 : 2);  // G * pq the kernel serves
+    while (G * pq * 2 <= max_cols && pq * 2 <= batch && mfma_serves(D, G * pq * 2, sb_dtype))
+      pq *= 2;
+  }
+  pl.pq = pq;
+  int eff_len = max_len;
+  if (mode == 0 && window > 0) eff_len = std::min(max_len, window);
+  if (prefill && window > 0) eff_len = std::min(max_len, window + pq - 1);
+  // (a prefill's queries are many short-to-long sequences: no minimum split)
+  const int min_splits = prefill ? 1 : min_splits_for(batch);
+  pl.chunk = plan_chunk(eff_len, groups, min_splits);
+  pl.max_splits = max_splits_bound(eff_len, groups, min_splits);
+  pl.wl = ws_layout(batch, Hq, D, pl.max_splits);
+  if (prefill && batch >= 64 && !o.prefill_splitk && prefill_tiles_serve(D, sb_dtype, gqa))
+    pl.kernel = SdpaKernel::prefill_tiles;
+  else if (hc)
+    pl.kernel = SdpaKernel::hc;
+  else if (try_mfma && mfma_serves(D, G * pq, sb_dtype))
+    pl.kernel = SdpaKernel::mfma;
+  else
+    pl.kernel = SdpaKernel::valu;
+  return pl;
+}
+
+const char* kernel_name(const SdpaPlan& pl, int D, int sb_dtype) {
+  (void)sb_dtype;
+  switch (pl.kernel) {
+    case SdpaKernel::prefill_tiles:
+      return (D != 512 && options().prefill_ws) ? "prefill_int4_ws_kernel" : "prefill_int4_kernel";
+    case SdpaKernel::hc:
+      return options().hc_one ? "sdpa_int4_hc_kernel" : "sdpa_int4_hc2_kernel";
+    case SdpaKernel::mfma: return "sdpa_int4_mfma_kernel";
+    default: return "sdpa_int4_kernel";
+  }
 }
 
 
@@ -401,39 +505,10 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
                "%s: k_quant / v_quant must be 16-byte aligned", fn);
   TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
 
-  // Matrix-core kernel when it serves (D, G); the VALU kernel otherwise or
-  // when TQ_SDPA_IMPL=valu forces it.  At D = 512 the matrix-core kernel
-  // takes at most 2 query heads per workgroup (2 heads x 8 quant groups fill
-  // its 16 columns): the head subgroups of one kv head then read the same
-  // K/V, concurrently and on one XCD (splits are a multiple of 8 at long
-  // contexts), so the repeats are served mostly from L2.  (The workspace
-  // bound of tq_sdpa_int4_workspace_size, planned with the largest subgroup,
-  // covers this: more groups never means more splits.)
-  const char* impl = std::getenv("TQ_SDPA_IMPL");
-  const bool try_mfma = !(impl && std::string(impl) == "valu");
-  // With GQA a multiple of 8, D = 512 runs the heads-as-columns kernel
-  // (8 heads per workgroup, each K/V byte unpacked once).
-  const bool hc = try_mfma && D == 512 && sb_dtype == TQ_F16 && gqa % 8 == 0;
-  int G = head_subgroup(gqa);
-  if (try_mfma && D == 512 && sb_dtype == TQ_F16 && !hc) G = gqa % 2 == 0 ? 2 : 1;
-  const int n_sub = gqa / G;
-  const int64_t groups = static_cast<int64_t>(batch) * Hkv * n_sub;
-  // Prefill on the matrix-core kernel: pq consecutive queries share a
-  // workgroup (its G * pq column sets fill the 16 MFMA columns), so each K/V
-  // byte serves pq queries.  Split planning stays per query, and a group's
-  // key range is the union of its windows (at most window + pq - 1 keys).
-  int pq = 1;
-  if (prefill && try_mfma && !hc && sb_dtype == TQ_F16) {
-    const int max_cols = D == 128 ? 8 : (D == 256 ? 4 : 2);  // G * pq the kernel serves
-    while (G * pq * 2 <= max_cols && pq * 2 <= batch) pq *= 2;
-  }
-  int eff_len = max_len;
-  if (!seq_lens && window > 0) eff_len = std::min(max_len, window + pq - 1);
-  // (a prefill's queries are many short-to-long sequences: no minimum split)
-  const int min_splits = prefill ? 1 : min_splits_for(batch);
-  const int chunk = plan_chunk(eff_len, groups, min_splits);
-  const int max_splits = max_splits_bound(eff_len, groups, min_splits);
-  const WsLayout wl = ws_layout(batch, Hq, D, max_splits);
+  const int mode = prefill ? 2 : (seq_lens ? 1 : 0);
+  const SdpaPlan pl = plan_sdpa(mode, batch, Hq, Hkv, D, max_len, gqa, window, sb_dtype);
+  const int n_sub = pl.n_sub, pq = pl.pq, max_splits = pl.max_splits;
+  const WsLayout wl = pl.wl;
   if (max_splits > 1) {
     if (!workspace || ws_bytes < wl.total) {
       set_error("%s: workspace of %zu bytes needed (got %zu)", fn, wl.total, ws_bytes);
@@ -462,7 +537,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   p.window = window;
   p.n_clamp = max_len;
   p.scale_log2 = scale * 1.4426950408889634f;
-  p.chunk = chunk;
+  p.chunk = pl.chunk;
   p.max_splits = max_splits;
   p.prefill = prefill;
   p.pq = pq;
@@ -470,30 +545,25 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
 
   dim3 grid(max_splits, Hkv * n_sub, (batch + pq - 1) / pq);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // A prefill of many queries runs the tile kernel (each K/V tile serves 64
-  // rows); short ones, and shapes it does not serve, the decode kernels.
-  // TQ_PREFILL_IMPL=splitk forces the latter.
-  const char* pimpl = std::getenv("TQ_PREFILL_IMPL");
-  if (prefill && batch >= 64 && !(pimpl && std::string(pimpl) == "splitk")) {
-    const int r = launch_prefill_tiles(p, D, sb_dtype, s);
-    if (r >= 0) return r;
-  }
-  if (hc) {
-    // 8 heads x 512 dims of partials per split: merged by a separate,
-    // parallel kernel rather than one workgroup per kv head
-    p.ext_merge = max_splits > 1 ? 1 : 0;
-    const int r = launch_sdpa_hc(p, grid, s);
-    if (r != TQ_OK || !p.ext_merge) return r;
-    return launch_merge_splits(p, D, batch, s);
-  }
-  if (try_mfma) {
-    const int r = launch_sdpa_mfma(p, D, G * pq, sb_dtype, grid, s);
-    if (r >= 0) return r;
-  }
-  switch (D) {
-    case 128: return launch_d<128>(p, G, sb_dtype, grid, s);
-    case 256: return launch_d<256>(p, G, sb_dtype, grid, s);
-    default: return launch_d<512>(p, G, sb_dtype, grid, s);
+  switch (pl.kernel) {
+    case SdpaKernel::prefill_tiles:
+      return launch_prefill_tiles(p, D, sb_dtype, s);
+    case SdpaKernel::hc: {
+      // 8 heads x 512 dims of partials per split: merged by a separate,
+      // parallel kernel rather than one workgroup per kv head
+      p.ext_merge = max_splits > 1 ? 1 : 0;
+      const int r = launch_sdpa_hc(p, grid, s);
+      if (r != TQ_OK || !p.ext_merge) return r;
+      return launch_merge_splits(p, D, batch, s);
+    }
+    case SdpaKernel::mfma:
+      return launch_sdpa_mfma(p, D, pl.G * pq, sb_dtype, grid, s);
+    default:
+      switch (D) {
+        case 128: return launch_d<128>(p, pl.G, sb_dtype, grid, s);
+        case 256: return launch_d<256>(p, pl.G, sb_dtype, grid, s);
+        default: return launch_d<512>(p, pl.G, sb_dtype, grid, s);
+      }
   }
 }
 
@@ -510,6 +580,37 @@ extern "C" size_t tq_sdpa_int4_workspace_size(int batch, int num_heads, int num_
   const int64_t groups = static_cast<int64_t>(batch) * num_kv_heads * (gqa / G);
   const int splits = max_splits_bound(max_kv_len, groups, min_splits_for(batch));
   return ws_layout(batch, num_heads, head_dim, splits).total;
+}
+
+extern "C" int tq_sdpa_int4_plan(int mode, int batch, int num_heads, int num_kv_heads,
+                                 int head_dim, int max_kv_len, tq_dtype sb_dtype,
+                                 int sliding_window, int* splits, int* chunk_keys,
+                                 char* kernel, size_t kernel_bytes) {
+  clear_error();
+  const char* fn = "tq_sdpa_int4_plan";
+  TQ_CHECK_ARG(mode >= 0 && mode <= 2, "%s: mode must be 0 (decode), 1 (ragged) or 2 (prefill)", fn);
+  TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32, "%s: sb_dtype must be f16 or f32", fn);
+  TQ_CHECK_ARG(head_dim == 128 || head_dim == 256 || head_dim == 512, "%s: bad head_dim %d", fn,
+               head_dim);
+  TQ_CHECK_ARG(batch >= 1 && num_kv_heads >= 1 && num_heads >= num_kv_heads &&
+                   num_heads % num_kv_heads == 0 && max_kv_len >= 0 && sliding_window >= 0,
+               "%s: bad shape", fn);
+  const SdpaPlan pl = plan_sdpa(mode, batch, num_heads, num_kv_heads, head_dim, max_kv_len,
+                                num_heads / num_kv_heads, sliding_window, sb_dtype);
+  if (splits) *splits = pl.max_splits;
+  if (chunk_keys) *chunk_keys = pl.chunk;
+  if (kernel && kernel_bytes > 0) {
+    const char* name = kernel_name(pl, head_dim, sb_dtype);
+    std::snprintf(kernel, kernel_bytes, "%s", name);
+  }
+  return TQ_OK;
+}
+
+extern "C" int tq_reload_options(void) {
+  clear_error();
+  options();  // the first read, if not done yet
+  read_options();
+  return TQ_OK;
 }
 
 extern "C" int tq_sdpa_int4(const void* q, tq_dtype q_dtype, const uint32_t* k_quant,

@@ -328,12 +328,51 @@ struct WsLayout {
 };
 
 int target_wgs();                                   // CUs of the current device
-int env_int(const char* name, int dflt);
 int head_subgroup(int gqa);                         // query heads per workgroup
 int plan_chunk(int max_len, int64_t groups, int min_splits);        // keys per workgroup
 int max_splits_bound(int max_len, int64_t groups, int min_splits);  // bound of ceil(L / chunk)
 int min_splits_for(int batch);                                      // 5 for batched launches
 WsLayout ws_layout(int batch, int Hq, int D, int max_splits);
+
+// Kernel-choice switches for tests and measurement.  They are read from the
+// environment once per process; tq_reload_options() reads them again.
+//   TQ_SDPA_IMPL=valu       the VALU decode kernel for every shape
+//   TQ_SDPA_CHUNK=n         keys per split (overrides the planner)
+//   TQ_PREFILL_IMPL=splitk  prefill on the split-K decode kernels
+//   TQ_PREFILL_WS=0         the one-role prefill tile kernel
+//   TQ_HC_IMPL=1            the one-wave D=512 heads-as-columns kernel
+struct Options {
+  bool sdpa_valu;
+  int sdpa_chunk;
+  bool prefill_splitk;
+  bool prefill_ws;
+  bool hc_one;
+};
+Options options();
+
+// Which kernel a decode / ragged / prefill call launches, and its split plan.
+enum class SdpaKernel { valu, mfma, hc, prefill_tiles };
+struct SdpaPlan {
+  SdpaKernel kernel;
+  int G;           // query heads per workgroup (before query grouping)
+  int n_sub;       // workgroups per kv head along the head axis (gqa / G)
+  int pq;          // consecutive prefill queries per workgroup (1 otherwise)
+  int chunk;       // keys per split
+  int max_splits;  // grid.x: bound of the splits of any sequence
+  WsLayout wl;     // workspace layout
+};
+// mode: 0 single sequence (n = kv_len), 1 ragged batch (max_len bounds the
+// lengths), 2 prefill (batch = queries, max_len = n_prior + n_new).
+SdpaPlan plan_sdpa(int mode, int batch, int Hq, int Hkv, int D, int max_len, int gqa, int window,
+                   int sb_dtype);
+const char* kernel_name(const SdpaPlan& pl, int D, int sb_dtype);
+
+// (D, query columns) served by the matrix-core kernel, for a scale dtype.
+bool mfma_serves(int D, int cols, int sb_dtype);
+// Scale dtypes the D = 512 heads-as-columns kernels serve.
+bool hc_serves(int sb_dtype);
+// Shapes the prefill tile kernels serve.
+bool prefill_tiles_serve(int D, int sb_dtype, int gqa);
 
 // Launch of the matrix-core kernel (tq_sdpa_mfma.hip).  Returns TQ_OK,
 // a tq_status error, or -1 when (D, G) is not served by that kernel.

@@ -902,10 +902,11 @@ int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t s) {
   return TQ_OK;
 }
 
+bool hc_serves(int sb_dtype) { return sb_dtype == TQ_F16; }
+
 int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t s) {
-  // TQ_HC_IMPL=1 selects the one-wave-per-SIMD kernel (read per call)
-  const char* impl = std::getenv("TQ_HC_IMPL");
-  const bool one = impl && impl[0] == '1';
+  // TQ_HC_IMPL=1 selects the one-wave-per-SIMD kernel
+  const bool one = options().hc_one;
   if (one) {
     sdpa_int4_hc_kernel<<<grid, kHcWaves * 64, 0, s>>>(p);
     TQ_CHECK_LAUNCH("sdpa_int4_hc_kernel");

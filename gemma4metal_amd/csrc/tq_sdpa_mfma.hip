@@ -43,7 +43,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
-template <int D, int G>
+template <int D, int G, bool F32>
 struct MGeom {
   static constexpr int NG = D / 64;     // quant groups per row
   static constexpr int COLS = G * NG;   // used MFMA columns
@@ -56,16 +56,23 @@ struct MGeom {
   static constexpr int VS = D == 512 ? 2 : 1;
   static constexpr int VWH = VW / VS;   // V words per lane per key of one wave
   static constexpr int VM = 8 * VWH;    // P.V accumulator tiles of one wave
-  static constexpr int SCW = NG / 2;    // 32-bit words of one key's scales
+  // 32-bit words of one key's scales (or biases): fp16 pairs, or fp32
+  static constexpr int SCW = F32 ? NG : NG / 2;
+  // Packed columns: with at most 8 (head, group) columns, the two 16-key
+  // tiles of an iteration share one K accumulator (tile 0 in columns 0-7,
+  // tile 1 in columns 8-15), and the P.V weights' bf16 hi and lo parts go
+  // to columns n and n + 8 of one product (one product per A tile instead
+  // of two).  Every score-epilogue lane then holds a used column.
+  static constexpr bool PACK = COLS <= 8 && VS == 1;
   static_assert(COLS <= 16, "more than 16 (head, group) columns");
   static_assert(D == 128 || D == 256 || D == 512, "D");
 };
 
-template <int D>
+template <int D, bool F32>
 struct IterBuf {
   uint32_t kw[2][D / 32];   // [tile][word] K slice of key (t0 + 16*tile + m)
   uint32_t vw[8][D / 128 / (D == 512 ? 2 : 1)];  // [slot][word] this wave's V words of key(slot)
-  uint32_t sc[2][D / 128];  // scales of keys (t0 + 2k, t0 + 2k + 1) of array l/16
+  uint32_t sc[2][F32 ? D / 64 : D / 128];  // scales of keys (t0 + 2k, t0 + 2k + 1) of array l/16
 };
 
 // Per-lane row offsets (in keys) inside one 32-key iteration.
@@ -88,12 +95,12 @@ __device__ __forceinline__ T stream_load(const T* p) {
 // `last` with one v_min against a uniform limit (only the final, partial
 // iteration of a wave is affected), and addressed as a uniform base plus a
 // 32-bit lane offset.
-template <int D, int G, bool kNT>
-__device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0,
+template <int D, int G, bool F32, bool kNT>
+__device__ __forceinline__ void load_iter(IterBuf<D, F32>& B, const uint32_t* kq_row0,
                                           const uint32_t* vq_row0, const uint32_t* sc_arr,
                                           const LaneRows& lr, int t0, int last, int m, int c,
                                           int vhalf) {
-  using Gm = MGeom<D, G>;
+  using Gm = MGeom<D, G, F32>;
   constexpr uint32_t RB = D / 2;  // bytes per packed row
   const int lim = last - t0;      // uniform; >= 0 for every issued iteration
   const char* kb = reinterpret_cast<const char*>(kq_row0 + static_cast<int64_t>(t0) * (D / 8));
@@ -125,9 +132,12 @@ __device__ __forceinline__ void load_iter(IterBuf<D>& B, const uint32_t* kq_row0
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const uint32_t off = static_cast<uint32_t>(min(lr.s[e], lim)) * (Gm::SCW * 4);
-    if constexpr (Gm::SCW == 4) {
-      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(sb + off));
-      B.sc[e][0] = u.x; B.sc[e][1] = u.y; B.sc[e][2] = u.z; B.sc[e][3] = u.w;
+    if constexpr (Gm::SCW >= 4) {
+#pragma unroll
+      for (int w = 0; w < Gm::SCW; w += 4) {
+        const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(sb + off + 4 * w));
+        B.sc[e][w] = u.x; B.sc[e][w + 1] = u.y; B.sc[e][w + 2] = u.z; B.sc[e][w + 3] = u.w;
+      }
     } else if constexpr (Gm::SCW == 2) {
       const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(sb + off));
       B.sc[e][0] = u.x; B.sc[e][1] = u.y;
@@ -150,15 +160,19 @@ __device__ __forceinline__ float half_hi(uint32_t w) {
 // p.pq consecutive queries, each column with its own causal / window limit.
 // Decode and single-query prefill use kQG = false.
 // kStreamNT: non-temporal K/V loads (see stream_load).
-template <int D, int G, int NW, bool kQG, bool kStreamNT>
+// F32: fp32 scale/bias (the reference's cache dtype); fp16 otherwise.
+template <int D, int G, int NW, bool kQG, bool kStreamNT, bool F32>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void sdpa_int4_mfma_kernel(SdpaParams p) {
   constexpr int kNT = NW * 64;       // threads per workgroup
-  constexpr int kIter = 32 * (NW / MGeom<D, G>::VS);  // keys per workgroup iteration
-  using Gm = MGeom<D, G>;
+  using Gm = MGeom<D, G, F32>;
+  constexpr int kIter = 32 * (NW / Gm::VS);  // keys per workgroup iteration
   constexpr int NG = Gm::NG, COLS = Gm::COLS, KM = Gm::KM, VW = Gm::VW, VM = Gm::VM;
   constexpr int VS = Gm::VS, VWH = Gm::VWH;
+  constexpr bool PACK = Gm::PACK;
+  constexpr int NTB = PACK ? 2 : 1;      // B-operand images of the K products
+  constexpr int SKP = F32 ? 32 : 16;     // staged scale slots per (array, group)
   constexpr int NWK = NW / VS;       // waves per key stream
   constexpr int RW = D / 8;
   constexpr int NE = (G * D + kNT - 1) / kNT;  // q elements per thread
@@ -166,7 +180,11 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   pin_args(p);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;  // A row / B,C column; lane group
-  const int n = m;                         // this lane's (head, group) column
+  // This lane's (head, group) column, and with packed columns the key tile
+  // of its scores (tile T's keys in C columns 8T .. 8T + 7) and the weight
+  // part it feeds the P.V products (0: bf16 hi, 1: bf16 lo).
+  const int n = PACK ? (m & 7) : m;
+  const int T = PACK ? (m >> 3) : 0;
   const int hn = n / NG, gn = n - (n / NG) * NG;
   const bool col_used = n < COLS;
   const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
@@ -187,10 +205,15 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int col_hi = pos;
   const int col_lo = p.window > 0 ? pos - p.window + 1 : 0;
 
-  using Fin = Finalize<G, D, NW>;
-  __shared__ float arena[Fin::kArena];
-  __shared__ uint32_t sc_lds[NW][4][NG][16];  // [wave][array][group][key pair] fp16x2
-  __shared__ uint4 bk_lds[3][KM][64];            // B operands of the K MFMAs
+  // With packed columns each wave leaves two partial results, the hi- and
+  // lo-part columns' products (slots wave and wave + NW), summed by the
+  // workgroup merge.
+  using Fin = Finalize<G, D, PACK ? 2 * NW : NW, NW * 64>;
+  __shared__ __align__(16) float arena[Fin::kArena];
+  // scales staged per wave as [array][group][key pair] fp16x2, or
+  // [array][group][key] fp32
+  __shared__ __align__(16) uint32_t sc_lds[NW][4][NG][SKP];
+  __shared__ uint4 bk_lds[NTB][3][KM][64];       // B operands of the K MFMAs
   __shared__ float red_max[NE][NW];
   __shared__ float sh_qhat[G][NG];
   __shared__ int sh_F[G];
@@ -247,9 +270,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // every outstanding load at the join): rows are clamped into
   // [0, max(last, 0)], valid memory even for a wave or split with no keys
   // (capacity >= 1).
-  IterBuf<D> bufA, bufB;
+  IterBuf<D, F32> bufA, bufB;
   const int safe_last = max(last, 0);
-  load_iter<D, G, kStreamNT>(bufA, kq_row0, vq_row0, sc_arr, lr, min(base0, safe_last), safe_last, m, c,
+  load_iter<D, G, F32, kStreamNT>(bufA, kq_row0, vq_row0, sc_arr, lr, min(base0, safe_last), safe_last, m, c,
                   vhalf);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -269,13 +292,13 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     if (lane == 0) red_max[k][wave] = mx;
   }
   {
-    uint4* z = &bk_lds[0][0][0];
-    for (int i = threadIdx.x; i < 3 * KM * 64; i += kNT) z[i] = uint4{0u, 0u, 0u, 0u};
+    uint4* z = &bk_lds[0][0][0][0];
+    for (int i = threadIdx.x; i < NTB * 3 * KM * 64; i += kNT) z[i] = uint4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
   // Every wave slot (k, w) holds 64 consecutive elements: one quant group of
   // one head, since 64 | D and 64 | kNT.
-  uint8_t* bk_bytes = reinterpret_cast<uint8_t*>(&bk_lds[0][0][0]);
+  uint8_t* bk_bytes = reinterpret_cast<uint8_t*>(&bk_lds[0][0][0][0]);
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
     const int e0 = wave * 64 + k * kNT;  // first element of this wave slot
@@ -306,6 +329,12 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       bk_bytes[byte0] = static_cast<uint8_t>(d0);
       bk_bytes[byte0 + KM * 64 * 16] = static_cast<uint8_t>(d1);
       bk_bytes[byte0 + 2 * KM * 64 * 16] = static_cast<uint8_t>(d2);
+      if constexpr (PACK) {  // tile 1's image: the same digits in column nn + 8
+        const int byte1 = byte0 + 3 * KM * 64 * 16 + 8 * 16;
+        bk_bytes[byte1] = static_cast<uint8_t>(d0);
+        bk_bytes[byte1 + KM * 64 * 16] = static_cast<uint8_t>(d1);
+        bk_bytes[byte1 + 2 * KM * 64 * 16] = static_cast<uint8_t>(d2);
+      }
       const int gsum = wave_sum_dpp(X);  // exact: 64 * 2^22 < 2^31
       if (lane == 0) {
         sh_qhat[h][d >> 6] = static_cast<float>(gsum) * ldexpf(1.0f, -F);
@@ -327,35 +356,39 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   uint32_t magic = 0x43004300u;
   asm volatile("" : "+v"(magic));
 
-  auto process = [&](const IterBuf<D>& B, int t0) {
-    // scales -> LDS [array][group][key], then this lane's 8 keys x 4 arrays
+  // The 4 staged scales of array a, group g, keys 16 * tile + 4c + {0..3}.
+  auto scale4 = [&](int a, int g, int tile) -> v4f {
+    if constexpr (F32) {
+      return *reinterpret_cast<const v4f*>(&sc_lds[wv][a][g][16 * tile + 4 * c]);
+    } else {
+      const uint2 u = *reinterpret_cast<const uint2*>(&sc_lds[wv][a][g][8 * tile + 2 * c]);
+      return v4f{half_lo(u.x), half_hi(u.x), half_lo(u.y), half_hi(u.y)};
+    }
+  };
+
+  auto process = [&](const IterBuf<D, F32>& B, int t0) {
+    // scales -> LDS [array][group][key]
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const uint32_t a0 = B.sc[0][g >> 1], a1 = B.sc[1][g >> 1];
-      const uint32_t v = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u))
-                                 : ((a0 & 0xFFFFu) | (a1 << 16));
-      sc_lds[wv][arr][g][k16] = v;
+      if constexpr (F32) {
+        *reinterpret_cast<uint2*>(&sc_lds[wv][arr][g][2 * k16]) = uint2{B.sc[0][g], B.sc[1][g]};
+      } else {
+        const uint32_t a0 = B.sc[0][g >> 1], a1 = B.sc[1][g >> 1];
+        const uint32_t v = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u))
+                                   : ((a0 & 0xFFFFu) | (a1 << 16));
+        sc_lds[wv][arr][g][k16] = v;
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    uint32_t scv[4][2][2];  // [array][tile][pair] = keys 16*tile + 4c + {0,1} / {2,3}
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int tile = 0; tile < 2; ++tile) {
-        const uint2 u = *reinterpret_cast<const uint2*>(&sc_lds[wv][a][gn][8 * tile + 2 * c]);
-        scv[a][tile][0] = u.x;
-        scv[a][tile][1] = u.y;
-      }
 
-    // K . q on the int8 matrix cores, 16 keys per tile
-    float sc[8];
-#pragma unroll
-    for (int tile = 0; tile < 2; ++tile) {
-      v4i acc[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) acc[k] = v4i{0, 0, 0, 0};
+    // K . q on the int8 matrix cores.  Score slot 4*u + i of this lane is key
+    // t0 + 16*tile(u) + 4c + i of column n: tile(u) = T with packed columns
+    // (one score tile), u otherwise (two).
+    constexpr int NU = PACK ? 1 : 2;
+    float sc[4 * NU];
+    auto kq_tile = [&](int tile, v4i (&acc)[3], int img) {
 #pragma unroll
       for (int i = 0; i < KM; ++i) {
         const uint32_t w0 = B.kw[tile][2 * i], w1 = B.kw[tile][2 * i + 1];
@@ -367,33 +400,51 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         for (int k = 0; k < 3; ++k) {
           // B operands live in LDS (16 B per lane per MFMA) to keep the wave
           // within 256 registers
-          const uint4 u = bk_lds[k][i][lane];
+          const uint4 u = bk_lds[img][k][i][lane];
           const v4i bq = v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z),
                              static_cast<int>(u.w)};
           acc[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, acc[k], 0, 0, 0);
         }
       }
+    };
+    auto scores = [&](const v4i (&acc)[3], int u, int tile) {
+      const v4f ks = scale4(0, gn, tile), kb = scale4(1, gn, tile);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
         const int lo01 = acc[0][i] + (acc[1][i] << 8);
         const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc[2][i]);
-        const uint32_t kspair = scv[0][tile][i >> 1], kbpair = scv[1][tile][i >> 1];
-        const float ks = (i & 1) ? half_hi(kspair) : half_lo(kspair);
-        const float kb = (i & 1) ? half_hi(kbpair) : half_lo(kbpair);
-        float part = dot * (ks * sf) + kb * qhat;
+        float part = dot * (ks[i] * sf) + kb[i] * qhat;
         part = group_sum<NG>(part);
         const int t = t0 + 16 * tile + 4 * c + i;
         bool keep = t < t_end && col_used;
         if constexpr (kQG) keep = keep && t <= col_hi && t >= col_lo;
-        sc[4 * tile + i] = keep ? part : -INFINITY;
+        sc[4 * u + i] = keep ? part : -INFINITY;
+      }
+    };
+    if constexpr (PACK) {
+      v4i acc[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) acc[k] = v4i{0, 0, 0, 0};
+      kq_tile(0, acc, 0);
+      kq_tile(1, acc, 1);
+      scores(acc, 0, T);
+    } else {
+#pragma unroll
+      for (int tile = 0; tile < 2; ++tile) {
+        v4i acc[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) acc[k] = v4i{0, 0, 0, 0};
+        kq_tile(tile, acc, 0);
+        scores(acc, tile, tile);
       }
     }
 
     // online softmax over the 32 keys (log2 domain)
     float mt = sc[0];
 #pragma unroll
-    for (int j = 1; j < 8; ++j) mt = fmaxf(mt, sc[j]);
+    for (int j = 1; j < 4 * NU; ++j) mt = fmaxf(mt, sc[j]);
+    if constexpr (PACK) mt = fmaxf(mt, ror8(mt));
     mt = xor16_max(mt);
     mt = xor32_max(mt);
     const float m_new = fmaxf(m_run, mt);
@@ -408,21 +459,48 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       for (int ff = 0; ff < VM; ++ff) cv[ff] *= f;
       m_run = m_new;
     }
+    // weights of this lane's own scores; the denominator and the V bias
+    // term count each key once (the lane of its score)
+    float pw[4 * NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const v4f vb = scale4(3, gn, PACK ? T : u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pj = sc[4 * u + i] == -INFINITY ? 0.0f : fast_exp2(sc[4 * u + i] - m_run);
+        pw[4 * u + i] = pj;
+        l_run += pj;
+        bacc = fmaf(pj, vb[i], bacc);
+      }
+    }
+    // the weights of the P.V k-slots: slot j = key 16*(j/4) + 4c + j%4
+    float ps[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (PACK) {
+        const float other = ror8(pw[i]);  // the other tile's key, same column
+        ps[i] = T ? other : pw[i];
+        ps[4 + i] = T ? pw[i] : other;
+      } else {
+        ps[i] = pw[i];
+        ps[4 + i] = pw[4 + i];
+      }
+    }
+    const v4f vs0 = scale4(2, gn, 0), vs1 = scale4(2, gn, 1);
     __bf16 hi[8], lo[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int tile = j >> 2, i = j & 3;
-      const float pj = sc[j] == -INFINITY ? 0.0f : fast_exp2(sc[j] - m_run);
-      l_run += pj;
-      const uint32_t vspair = scv[2][tile][i >> 1], vbpair = scv[3][tile][i >> 1];
-      const float vs = (i & 1) ? half_hi(vspair) : half_lo(vspair);
-      const float vb = (i & 1) ? half_hi(vbpair) : half_lo(vbpair);
-      bacc = fmaf(pj, vb, bacc);
-      const float w = pj * vs;
+      const float w = ps[j] * (j < 4 ? vs0[j] : vs1[j - 4]);
       hi[j] = static_cast<__bf16>(w);
       const float hf = static_cast<float>(hi[j]);
       lo[j] = static_cast<__bf16>(w - hf);
-      wsum += hf + static_cast<float>(lo[j]);
+      if constexpr (PACK) {
+        // column n + 8T takes part T of the weight
+        hi[j] = T ? lo[j] : hi[j];
+        wsum += static_cast<float>(hi[j]);
+      } else {
+        wsum += hf + static_cast<float>(lo[j]);
+      }
     }
     const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
     const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
@@ -450,14 +528,16 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         const int fe = 8 * s + 2 * by, fo = fe + 1;
         cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, bhi, cv[fe], 0, 0, 0);
         cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, bhi, cv[fo], 0, 0, 0);
-        cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, blo, cv[fe], 0, 0, 0);
-        cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, blo, cv[fo], 0, 0, 0);
+        if constexpr (!PACK) {
+          cv[fe] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, blo, cv[fe], 0, 0, 0);
+          cv[fo] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, blo, cv[fo], 0, 0, 0);
+        }
       }
     }
   };
 
-  auto load_next = [&](IterBuf<D>& B, int t0) {
-    load_iter<D, G, kStreamNT>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c, vhalf);
+  auto load_next = [&](IterBuf<D, F32>& B, int t0) {
+    load_iter<D, G, F32, kStreamNT>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c, vhalf);
   };
 
   auto pace = [&](int done) { pace_waves<NW>(s_done, wv, lane, done); };
@@ -499,31 +579,47 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   wsum = xor32_sum(wsum);
   bacc = xor16_sum(bacc);
   bacc = xor32_sum(bacc);
+  if constexpr (PACK) {
+    // columns n and n + 8 hold tile 0's / tile 1's keys (denominator, bias
+    // term): add the two; the hi / lo weight parts' products stay in their
+    // own lanes and arena slots, each with its own 128 offset removed
+    l_sum += ror8(l_sum);
+    bacc += ror8(bacc);
+    if (T) bacc = 0.0f;  // counted once, in the hi-part slot
+  }
+  const int slot = wave + (PACK ? T * NW : 0);
   if (col_used) {
-    // a wave's arena slot covers every dim: its own V words' dims get the
-    // result, the other V half's dims zero; only V half 0 counts the
-    // denominator (both halves scored the same keys)
+    // Accumulator element (s, j) of C row 4c + i is dim 8 * (VW * (4c + i) +
+    // s) + j: for one (c, i) the 8 * VW dims are contiguous and lie in one
+    // quant group, so a lane writes the rows of its column's group as whole
+    // vectors.  A wave's arena slot covers every dim: its own V words' dims
+    // get the result, the other V half's dims zero; only V half 0 counts the
+    // denominator (both halves scored the same keys).
 #pragma unroll
-    for (int sg = 0; sg < VW; ++sg)
+    for (int i = 0; i < 4; ++i) {
+      const int dim0 = 8 * VW * (4 * c + i);
+      if ((dim0 >> 6) == gn) {
+        float row[8 * VW];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+        for (int sg = 0; sg < VW; ++sg)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int dim = 8 * (VW * (4 * c + i) + sg) + j;
-          if ((dim >> 6) == gn) {
-            const int s = sg - vhalf * VWH;  // this wave's word index, if owned
+          for (int j = 0; j < 8; ++j) {
+            const int so = sg - vhalf * VWH;  // this wave's word index, if owned
             float v = 0.0f;
 #pragma unroll
-            for (int so = 0; so < VWH; ++so)
-              if (so == s) {
-                v = (cv[8 * so + j][i] - 128.0f * wsum) + bacc;
-              }
-            Fin::o(arena, wave, hn)[dim] = v;
+            for (int s2 = 0; s2 < VWH; ++s2)
+              if (s2 == so) v = (cv[8 * s2 + j][i] - 128.0f * wsum) + bacc;
+            row[8 * sg + j] = v;
           }
-        }
+        v4f* dst = reinterpret_cast<v4f*>(Fin::o(arena, slot, hn) + dim0);
+#pragma unroll
+        for (int q4 = 0; q4 < 2 * VW; ++q4)
+          dst[q4] = v4f{row[4 * q4], row[4 * q4 + 1], row[4 * q4 + 2], row[4 * q4 + 3]};
+      }
+    }
     if (gn == 0 && c == 0) {
-      Fin::m(arena, wave)[hn] = m_run;
-      Fin::l(arena, wave)[hn] = vhalf == 0 ? l_sum : 0.0f;
+      Fin::m(arena, slot)[hn] = m_run;
+      Fin::l(arena, slot)[hn] = (vhalf == 0 && T == 0) ? l_sum : 0.0f;
     }
   }
   if constexpr (kQG)
@@ -533,36 +629,49 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
 }
 
-template <int D, int G>
-int launch_dg(const SdpaParams& p, dim3 grid, hipStream_t s) {
+template <int D, int G, bool F32>
+int launch_dgs(const SdpaParams& p, dim3 grid, hipStream_t s) {
   constexpr int NW = D == 512 ? 4 : kMfmaWaves;
   if (p.prefill && p.pq > 1)
-    sdpa_int4_mfma_kernel<D, G, NW, true, true><<<grid, NW * 64, 0, s>>>(p);
+    sdpa_int4_mfma_kernel<D, G, NW, true, true, F32><<<grid, NW * 64, 0, s>>>(p);
   else if (p.seq_lens)  // batched sequences of their own lengths
-    sdpa_int4_mfma_kernel<D, G, NW, false, false><<<grid, NW * 64, 0, s>>>(p);
+    sdpa_int4_mfma_kernel<D, G, NW, false, false, F32><<<grid, NW * 64, 0, s>>>(p);
   else
-    sdpa_int4_mfma_kernel<D, G, NW, false, true><<<grid, NW * 64, 0, s>>>(p);
+    sdpa_int4_mfma_kernel<D, G, NW, false, true, F32><<<grid, NW * 64, 0, s>>>(p);
   TQ_CHECK_LAUNCH("sdpa_int4_mfma_kernel");
   return TQ_OK;
 }
 
+template <int D, int G>
+int launch_dg(const SdpaParams& p, int sb_dtype, dim3 grid, hipStream_t s) {
+  return sb_dtype == TQ_F32 ? launch_dgs<D, G, true>(p, grid, s) : launch_dgs<D, G, false>(p, grid, s);
+}
+
 }  // namespace
+
+bool mfma_serves(int D, int cols, int sb_dtype) {
+  if (sb_dtype != TQ_F16 && sb_dtype != TQ_F32) return false;
+  if (D == 256) return cols == 1 || cols == 2 || cols == 4;
+  if (D == 512) return cols == 1 || cols == 2;
+  if (D == 128) return cols == 1 || cols == 2 || cols == 4 || cols == 8;
+  return false;
+}
 
 int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
                      hipStream_t stream) {
-  if (sb_dtype != TQ_F16) return -1;
+  if (!mfma_serves(D, G, sb_dtype)) return -1;
   if (D == 256) {
-    if (G == 1) return launch_dg<256, 1>(p, grid, stream);
-    if (G == 2) return launch_dg<256, 2>(p, grid, stream);
-    if (G == 4) return launch_dg<256, 4>(p, grid, stream);
+    if (G == 1) return launch_dg<256, 1>(p, sb_dtype, grid, stream);
+    if (G == 2) return launch_dg<256, 2>(p, sb_dtype, grid, stream);
+    if (G == 4) return launch_dg<256, 4>(p, sb_dtype, grid, stream);
   } else if (D == 512) {
-    if (G == 1) return launch_dg<512, 1>(p, grid, stream);
-    if (G == 2) return launch_dg<512, 2>(p, grid, stream);
+    if (G == 1) return launch_dg<512, 1>(p, sb_dtype, grid, stream);
+    if (G == 2) return launch_dg<512, 2>(p, sb_dtype, grid, stream);
   } else if (D == 128) {
-    if (G == 1) return launch_dg<128, 1>(p, grid, stream);
-    if (G == 2) return launch_dg<128, 2>(p, grid, stream);
-    if (G == 4) return launch_dg<128, 4>(p, grid, stream);
-    if (G == 8) return launch_dg<128, 8>(p, grid, stream);
+    if (G == 1) return launch_dg<128, 1>(p, sb_dtype, grid, stream);
+    if (G == 2) return launch_dg<128, 2>(p, sb_dtype, grid, stream);
+    if (G == 4) return launch_dg<128, 4>(p, sb_dtype, grid, stream);
+    if (G == 8) return launch_dg<128, 8>(p, sb_dtype, grid, stream);
   }
   return -1;
 }

@@ -125,6 +125,30 @@ def sdpa_int4(queries: torch.Tensor,
     return out
 
 
+_PLAN_MODES = {"decode": 0, "ragged": 1, "prefill": 2}
+
+
+def sdpa_plan(num_heads: int, num_kv_heads: int, head_dim: int, max_kv_len: int, *,
+              sb_dtype: torch.dtype = torch.float16, mode: str = "decode", batch: int = 1,
+              sliding_window: int = 0) -> dict:
+    """The kernel a call of this shape launches and its split plan
+    (``tq_sdpa_int4_plan``; no GPU work): ``{"kernel", "splits", "chunk"}``."""
+    _need(sb_dtype in (torch.float16, torch.float32), "sb_dtype must be float16 or float32")
+    splits, chunk = ctypes.c_int(0), ctypes.c_int(0)
+    name = ctypes.create_string_buffer(64)
+    call("tq_sdpa_int4_plan", _PLAN_MODES[mode], int(batch), int(num_heads), int(num_kv_heads),
+         int(head_dim), int(max_kv_len), _DT[sb_dtype], int(sliding_window), ctypes.byref(splits),
+         ctypes.byref(chunk), name, len(name))
+    return {"kernel": name.value.decode(), "splits": splits.value, "chunk": chunk.value}
+
+
+def reload_options() -> None:
+    """Re-read the TQ_* kernel-choice switches from the environment (they
+    are read once per process otherwise)."""
+    call("tq_reload_options")
+    _decode_ws_size.cache_clear()
+
+
 @functools.lru_cache(maxsize=256)
 def _decode_ws_size(Hq: int, Hkv: int, D: int, n: int) -> int:
     """Workspace bytes of one single-sequence decode call (a pure function

@@ -58,6 +58,16 @@ int tq_sync(void);
  * attention kernel's roofline. */
 int tq_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
 
+/* Measurement utility (no counterpart in the reference): a streaming read in
+ * the decode-attention kernel's geometry -- `blocks` workgroups of `waves`
+ * wave64s, workgroup b reading the b-th contiguous slice of `bytes`, each
+ * lane issuing `loads_per_lane` 16-byte loads per iteration with `depth`
+ * iterations in flight, non-temporal when `nontemporal` != 0.  sink holds
+ * blocks * waves * 64 words.  (waves, loads_per_lane) is one of (8,4) (8,9)
+ * (8,16) (4,9) (4,16) (16,4) (16,9); depth is 1, 2 or 3. */
+int tq_stream_read_tiles(const void* src, size_t bytes, uint32_t* sink, int blocks, int waves,
+                         int loads_per_lane, int depth, int nontemporal, void* stream);
+
 /* ---- fused int4 decode attention ------------------------------------------
  * Replaces turboquant::sdpa_int4 (lib/turboquant.h:196-207,
  * lib/turboquant.cpp:367-417).  out[h] = softmax(scale * q[h] . K^T) V over
@@ -76,6 +86,24 @@ int tq_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, vo
  * batch * num_heads must not exceed 65536. */
 size_t tq_sdpa_int4_workspace_size(int batch, int num_heads, int num_kv_heads,
                                    int head_dim, int max_kv_len);
+
+/* Planning query (no counterpart in the reference, whose eval_gpu picks a
+ * kernel by name at lib/turboquant.cpp:376-379): the kernel a call with
+ * these arguments launches and its split plan, with no GPU work.  mode 0 =
+ * tq_sdpa_int4 (max_kv_len = kv_len), 1 = tq_sdpa_int4_ragged, 2 =
+ * tq_sdpa_int4_prefill (batch = n_new, max_kv_len = n_prior + n_new).
+ * *splits = workgroups per sequence along the keys (grid x), *chunk_keys =
+ * keys per split; the kernel's name is written to kernel[kernel_bytes]. */
+int tq_sdpa_int4_plan(int mode, int batch, int num_heads, int num_kv_heads, int head_dim,
+                      int max_kv_len, tq_dtype sb_dtype, int sliding_window, int* splits,
+                      int* chunk_keys, char* kernel, size_t kernel_bytes);
+
+/* Re-reads the kernel-choice switches from the environment (no counterpart
+ * in the reference).  They are read once per process otherwise:
+ * TQ_SDPA_IMPL=valu, TQ_SDPA_CHUNK=<keys>, TQ_PREFILL_IMPL=splitk,
+ * TQ_PREFILL_WS=0, TQ_HC_IMPL=1.  For tests and measurement; calls that run
+ * while it executes see the old or the new values. */
+int tq_reload_options(void);
 int tq_sdpa_int4(const void* q, tq_dtype q_dtype,
                  const uint32_t* k_quant, const void* k_scales, const void* k_biases,
                  const uint32_t* v_quant, const void* v_scales, const void* v_biases,

@@ -38,6 +38,38 @@ def test_sdpa_matches_oracle(gpu, Hq, Hkv, D, L, W, qdt, sb, scale):
     assert_close(host(out), ref, f"Hq{Hq} Hkv{Hkv} D{D} L{L} W{W}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,L,W", [
+    (32, 16, 256, 3000, 0),    # Gemma sliding layer shape, packed columns
+    (32, 16, 256, 1500, 1024), # window active
+    (2, 1, 128, 33, 0),        # the reference test shape
+    (32, 4, 256, 1500, 0),     # GQA 8 at D 256: two 4-head subgroups per kv head
+    (32, 4, 512, 2000, 0),     # Gemma global layer with fp32 scales: 2-head subgroups
+    (8, 8, 512, 700, 0),       # D 512, GQA 1
+    (16, 2, 128, 2100, 0),     # D 128, GQA 8: all 16 columns
+])
+def test_f32_scales_on_matrix_cores(gpu, Hq, Hkv, D, L, W):
+    """fp32 scale/bias, the reference's cache dtype (lib/turboquant.h:199,
+    fed by quantize at engine/gemma4_multilayer.cpp:228), runs on the
+    matrix-core kernel and matches the oracle."""
+    assert gpu.sdpa_plan(Hq, Hkv, D, L, sb_dtype=torch.float32,
+                         sliding_window=W)["kernel"] == "sdpa_int4_mfma_kernel"
+    rng = np.random.default_rng(Hq * 17 + L + D)
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    c = host_cache(rng, Hkv, L, D, "f32")
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv, 1.0, W)
+    assert_close(host(out), O.sdpa_int4(qv, *c, Hq // Hkv, 1.0, W), f"f32 s/b Hq{Hq} Hkv{Hkv} D{D}")
+
+
+def test_gqa8_d256_fp16(gpu):
+    rng = np.random.default_rng(88)
+    Hq, Hkv, D, L = 32, 4, 256, 2500
+    assert gpu.sdpa_plan(Hq, Hkv, D, L)["kernel"] == "sdpa_int4_mfma_kernel"
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    c = host_cache(rng, Hkv, L, D, "f16")
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], 8)
+    assert_close(host(out), O.sdpa_int4(qv, *c, 8), "GQA 8 D 256")
+
+
 def test_sdpa_prefix_of_capacity_and_repeat_calls(gpu):
     rng = np.random.default_rng(3)
     Hq, Hkv, D, cap = 32, 16, 256, 3000
@@ -395,7 +427,7 @@ def test_sdpa_prefill_tile_kernel(gpu, Hq, Hkv, D, S, prior, W, qdt):
 
 
 @pytest.mark.parametrize("Hq,Hkv,L,W", [(32, 4, 5000, 0), (32, 4, 3001, 1024), (16, 2, 129, 0)])
-def test_d512_one_wave_and_wave_specialised_kernels_agree(gpu, monkeypatch, Hq, Hkv, L, W):
+def test_d512_one_wave_and_wave_specialised_kernels_agree(gpu, tq_env, Hq, Hkv, L, W):
     """The two D=512 GQA-8 kernels (TQ_HC_IMPL=1 selects the one-wave one)
     compute the same products: outputs agree to fp32 rounding."""
     rng = np.random.default_rng(L + W)
@@ -403,14 +435,14 @@ def test_d512_one_wave_and_wave_specialised_kernels_agree(gpu, monkeypatch, Hq, 
     c = host_cache(rng, Hkv, L, 512, "f16")
     cd = [dev(a) for a in c]
     two = host(gpu.sdpa_int4(qd, *cd, Hq // Hkv, 1.0, W))
-    monkeypatch.setenv("TQ_HC_IMPL", "1")
+    tq_env("TQ_HC_IMPL", "1")
     one = host(gpu.sdpa_int4(qd, *cd, Hq // Hkv, 1.0, W))
     assert np.abs(two - one).max() < 1e-4
     assert_close(one, O.sdpa_int4(qv, *c, Hq // Hkv, 1.0, W), "one-wave D512")
 
 
 @pytest.mark.parametrize("D,gqa", [(256, 2), (128, 8)])
-def test_prefill_tile_kernels_agree(gpu, monkeypatch, D, gqa):
+def test_prefill_tile_kernels_agree(gpu, tq_env, D, gqa):
     """The wave-specialised and one-role tile kernels (TQ_PREFILL_WS=0)
     compute the same products in the same order: bit-identical outputs."""
     rng = np.random.default_rng(D + gqa)
@@ -419,41 +451,41 @@ def test_prefill_tile_kernels_agree(gpu, monkeypatch, D, gqa):
     c = host_cache(rng, Hkv, prior + S, D, "f16")
     cd = [dev(a) for a in c]
     ws = host(gpu.sdpa_int4_prefill(qd, *cd, prior, gqa, 1.0, W))
-    monkeypatch.setenv("TQ_PREFILL_WS", "0")
+    tq_env("TQ_PREFILL_WS", "0")
     one = host(gpu.sdpa_int4_prefill(qd, *cd, prior, gqa, 1.0, W))
     assert np.array_equal(ws, one)
     assert_close(ws, O.sdpa_int4_prefill(qv, *c, prior, gqa, 1.0, W), f"ws prefill D{D}")
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,L", [(32, 16, 256, 3000), (8, 2, 128, 1500), (8, 4, 512, 700)])
-def test_valu_kernel_forced_matches_oracle(gpu, monkeypatch, Hq, Hkv, D, L):
+def test_valu_kernel_forced_matches_oracle(gpu, tq_env, Hq, Hkv, D, L):
     """TQ_SDPA_IMPL=valu runs the VALU kernel for fp16 caches too."""
     rng = np.random.default_rng(D + L)
     qd, qv = queries(rng, (Hq, D), "bf16")
     c = host_cache(rng, Hkv, L, D, "f16")
-    monkeypatch.setenv("TQ_SDPA_IMPL", "valu")
+    tq_env("TQ_SDPA_IMPL", "valu")
     out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv)
     assert_close(host(out), O.sdpa_int4(qv, *c, Hq // Hkv), f"valu D{D} L{L}")
 
 
 @pytest.mark.parametrize("chunk", [128, 384, 4096])
-def test_forced_chunk_matches_oracle(gpu, monkeypatch, chunk):
+def test_forced_chunk_matches_oracle(gpu, tq_env, chunk):
     """TQ_SDPA_CHUNK overrides the split planner (more or fewer splits)."""
     rng = np.random.default_rng(chunk)
     Hq, Hkv, D, L = 32, 16, 256, 6000
     qd, qv = queries(rng, (Hq, D), "bf16")
     c = host_cache(rng, Hkv, L, D, "f16")
-    monkeypatch.setenv("TQ_SDPA_CHUNK", str(chunk))
+    tq_env("TQ_SDPA_CHUNK", str(chunk))
     out = gpu.sdpa_int4(qd, *[dev(a) for a in c], 2)
     assert_close(host(out), O.sdpa_int4(qv, *c, 2), f"chunk {chunk}")
 
 
-def test_sdpa_prefill_tile_and_split_paths_agree(gpu, monkeypatch):
+def test_sdpa_prefill_tile_and_split_paths_agree(gpu, tq_env):
     rng = np.random.default_rng(91)
     Hq, Hkv, D, S, prior, W = 32, 16, 256, 160, 500, 300
     qd, _ = queries(rng, (S, Hq, D), "bf16")
     cd = [dev(a) for a in host_cache(rng, Hkv, prior + S, D, "f16")]
     tiles = host(gpu.sdpa_int4_prefill(qd, *cd, prior, 2, 1.0, W))
-    monkeypatch.setenv("TQ_PREFILL_IMPL", "splitk")
+    tq_env("TQ_PREFILL_IMPL", "splitk")
     split = host(gpu.sdpa_int4_prefill(qd, *cd, prior, 2, 1.0, W))
     assert np.abs(tiles - split).max() < 1e-3
