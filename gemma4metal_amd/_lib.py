@@ -40,6 +40,7 @@ SIGNATURES = {
     "tq_stream_read_tiles": (I, [P, SZ, P, I, I, I, I, I, P]),
     "tq_sdpa_int4_workspace_size": (SZ, [I, I, I, I, I]),
     "tq_sdpa_int4_plan": (I, [I, I, I, I, I, I, I, I, P, P, P, SZ]),
+    "tq_sdpa_int4_noalloc": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, I, F, I, P]),
     "tq_reload_options": (I, []),
     "tq_sdpa_int4": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, I, F, I, P, SZ, P]),
     "tq_sdpa_int4_ragged": (I, [P, I, P, P, P, P, P, P, I, P, I, I, I, I, I, P, P, I, I, F, I,

@@ -613,6 +613,84 @@ extern "C" int tq_reload_options(void) {
   return TQ_OK;
 }
 
+// ---- decode with library-owned scratch (no caller workspace) -----------------
+//
+// tq_sdpa_int4_noalloc runs the same kernels as tq_sdpa_int4 with the split-K
+// workspace in a file-scope device array instead of a caller buffer, for
+// callers that cannot allocate (HIP graph capture, allocation-free serving
+// loops).  Each GPU the library runs on holds its own copy of `scratch` until
+// the process ends.  Host code never passes the array's name to a kernel: it
+// is a host-side stand-in, not a device address.  The device address comes
+// from hipGetSymbolAddress, once per device with that device current, and is
+// kept per device.
+namespace {
+constexpr size_t kScratchBytes = size_t{8} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Zeroes the split counters at the head of a fresh scratch array (the
+// array is zero at module load already; this makes the starting state
+// explicit).  A kernel, not hipMemsetAsync, so that a first call made under
+// graph capture records an ordinary kernel node.
+__global__ void zero_words_kernel(int* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// This device's scratch address (set up on the first call on the device).
+int device_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  TQ_CHECK_HIP(hipGetDevice(&dev));
+  TQ_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "tq_sdpa_int4_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    TQ_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    TQ_CHECK_ARG(ptr != nullptr, "tq_sdpa_int4_noalloc: no device address for the scratch array");
+    const int n = static_cast<int>(kMaxCounters);
+    zero_words_kernel<<<(n + 255) / 256, 256, 0, stream>>>(static_cast<int*>(ptr), n);
+    TQ_CHECK_LAUNCH("zero_words_kernel");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TQ_OK;
+}
+}  // namespace
+
+extern "C" int tq_sdpa_int4_noalloc(const void* q, tq_dtype q_dtype, const uint32_t* k_quant,
+                                    const void* k_scales, const void* k_biases,
+                                    const uint32_t* v_quant, const void* v_scales,
+                                    const void* v_biases, tq_dtype sb_dtype, float* out,
+                                    int num_heads, int num_kv_heads, int head_dim, int kv_len,
+                                    int kv_capacity, int gqa_factor, float scale,
+                                    int sliding_window, void* stream) {
+  clear_error();
+  const char* fn = "tq_sdpa_int4_noalloc";
+  // the scratch bound is checked before any device call
+  if ((head_dim == 128 || head_dim == 256 || head_dim == 512) && num_kv_heads >= 1 &&
+      gqa_factor >= 1 && num_heads == num_kv_heads * gqa_factor && kv_len >= 0 &&
+      sliding_window >= 0 && (sb_dtype == TQ_F16 || sb_dtype == TQ_F32)) {
+    const SdpaPlan pl = plan_sdpa(0, 1, num_heads, num_kv_heads, head_dim, kv_len, gqa_factor,
+                                  sliding_window, sb_dtype);
+    if (pl.max_splits > 1 && pl.wl.total > kScratchBytes) {
+      set_error("%s: this shape needs %zu bytes of split-K scratch, more than the library's "
+                "static %zu bytes; call tq_sdpa_int4 with a workspace instead",
+                fn, pl.wl.total, kScratchBytes);
+      return TQ_ERR_UNSUPPORTED;
+    }
+  }
+  void* ws = nullptr;
+  const int st = device_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (st != TQ_OK) return st;
+  return sdpa_common(q, q_dtype, k_quant, k_scales, k_biases, v_quant, v_scales, v_biases,
+                     sb_dtype, out, 1, num_heads, num_kv_heads, head_dim, kv_capacity, kv_len,
+                     nullptr, nullptr, kv_len, gqa_factor, scale, sliding_window, ws,
+                     kScratchBytes, stream, fn);
+}
+
 extern "C" int tq_sdpa_int4(const void* q, tq_dtype q_dtype, const uint32_t* k_quant,
                             const void* k_scales, const void* k_biases, const uint32_t* v_quant,
                             const void* v_scales, const void* v_biases, tq_dtype sb_dtype,

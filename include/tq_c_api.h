@@ -87,6 +87,22 @@ int tq_stream_read_tiles(const void* src, size_t bytes, uint32_t* sink, int bloc
 size_t tq_sdpa_int4_workspace_size(int batch, int num_heads, int num_kv_heads,
                                    int head_dim, int max_kv_len);
 
+/* tq_sdpa_int4 without a caller workspace.  No counterpart in the reference:
+ * for callers that cannot allocate (HIP graph capture, allocation-free
+ * serving loops).  The split-K workspace is a library-owned static device
+ * array of 8 MiB per GPU (held until the process ends), which covers every
+ * single-sequence decode shape under the default split planner; a shape
+ * that would need more returns TQ_ERR_UNSUPPORTED before any GPU work.
+ * Allocates nothing.  All calls on one GPU share its array: calls that
+ * overlap on one GPU (concurrent streams, or graphs replayed concurrently)
+ * race.  Arguments as tq_sdpa_int4. */
+int tq_sdpa_int4_noalloc(const void* q, tq_dtype q_dtype,
+                         const uint32_t* k_quant, const void* k_scales, const void* k_biases,
+                         const uint32_t* v_quant, const void* v_scales, const void* v_biases,
+                         tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
+                         int head_dim, int kv_len, int kv_capacity, int gqa_factor, float scale,
+                         int sliding_window, void* stream);
+
 /* Planning query (no counterpart in the reference, whose eval_gpu picks a
  * kernel by name at lib/turboquant.cpp:376-379): the kernel a call with
  * these arguments launches and its split plan, with no GPU work.  mode 0 =
