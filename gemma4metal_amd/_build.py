@@ -66,8 +66,10 @@ def build_cpp_tests() -> list:
     for name in CPP_TESTS:
         src = os.path.join(CPP_TEST_DIR, name + ".cpp")
         exe = os.path.join(CPP_TEST_DIR, name)
-        cmd = [_hipcc(), "-O2", "-std=c++17", f"-I{INCLUDE}", "-x", "c++", src, "-o", exe,
-               f"-L{HERE}", "-lturboquant_hip", "-Wl,-rpath,$ORIGIN/../../gemma4metal_amd"]
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        cmd = [_hipcc(), "-O2", "-std=c++17", f"-I{INCLUDE}", "-D__HIP_PLATFORM_AMD__",
+               f"-I{rocm}/include", "-x", "c++", src, "-o", exe, f"-L{HERE}", "-lturboquant_hip",
+               f"-L{rocm}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../gemma4metal_amd"]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stderr}")

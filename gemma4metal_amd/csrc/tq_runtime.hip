@@ -1,6 +1,7 @@
 // Library-level entry points: version, thread-local error string, and the
 // small device-memory helpers that let a ctypes caller drive the library
 // without any other GPU runtime.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 
@@ -39,6 +40,21 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
     acc ^= a.x ^ a.y ^ a.z ^ a.w;
   }
   sink[static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x] = acc;
+}
+
+__global__ void zero_words_kernel(uint32_t* p, size_t n) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+int zero_async(void* p, size_t bytes, hipStream_t s) {
+  TQ_CHECK_ARG(p != nullptr && bytes % 4 == 0, "zero_async: bad buffer");
+  const size_t n = bytes / 4;
+  const int blocks = static_cast<int>(std::min<size_t>((n + 255) / 256, 1024));
+  if (n) zero_words_kernel<<<blocks, 256, 0, s>>>(static_cast<uint32_t*>(p), n);
+  TQ_CHECK_LAUNCH("zero_words_kernel");
+  return TQ_OK;
 }
 
 // Streaming read in the decode-attention kernel's launch geometry: one

@@ -1,19 +1,26 @@
 // C++ API of include/turboquant.h over the C ABI of include/tq_c_api.h.
 //
 // Outputs are allocated here (the reference allocates inside eval_gpu,
-// lib/turboquant.cpp:372); the split-K workspace is one zero-filled buffer
-// per device, grown on demand under a mutex and reused (the kernels return
-// its counters to zero).  A call that grows it synchronises the device
-// first, so no queued kernel still uses the old buffer when it is freed.
+// lib/turboquant.cpp:372); the split-K workspace is a zero-filled buffer per
+// (device, stream), grown on demand with stream-ordered allocation and
+// reused (the kernels return its counters to zero).  sdpa_int4_into also
+// takes a caller-owned workspace.
 #include "turboquant.h"
 
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <mutex>
 #include <stdexcept>
-#include <unordered_map>
+#include <utility>
 
 #include "tq_c_api.h"
+
+namespace tq {
+// Zero-fills `bytes` (a multiple of 4) at p with a kernel on stream s
+// (tq_runtime.hip).
+int zero_async(void* p, size_t bytes, hipStream_t s);
+}  // namespace tq
 
 namespace turboquant {
 namespace {
@@ -42,26 +49,33 @@ tq_dtype c_dtype(Dtype d) {
 
 bool is_sb(Dtype d) { return d == Dtype::float32 || d == Dtype::float16; }
 
+// Split-K workspaces, one per (device, stream): calls on one stream run in
+// order, so they can share one; calls on different streams never do.  A
+// workspace that must grow is replaced by a stream-ordered allocation on that
+// stream, zero-filled by a kernel on the same stream, and the old buffer is
+// released with a stream-ordered free after the calls already queued there:
+// nothing synchronises the device, and no buffer is freed while a queued
+// kernel may still use it.
 struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::unordered_map<int, Workspace> g_ws;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-// Zero-filled split-K workspace of at least `bytes` on the current device.
-void* workspace(size_t bytes, size_t* have) {
+void* workspace(size_t bytes, size_t* have, StreamOrDevice s) {
   int dev = 0;
   check_hip(hipGetDevice(&dev), "hipGetDevice");
+  const hipStream_t stream = static_cast<hipStream_t>(s);
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  Workspace& w = g_ws[dev];
+  Workspace& w = g_ws[{dev, stream}];
   if (w.bytes < bytes) {
     const size_t nb = std::max<size_t>(bytes, size_t{1} << 20);
-    check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
-    if (w.ptr) check_hip(hipFree(w.ptr), "hipFree");
-    w.ptr = nullptr;
-    check_hip(hipMalloc(&w.ptr, nb), "hipMalloc");
-    check_hip(hipMemset(w.ptr, 0, nb), "hipMemset");
+    void* p = nullptr;
+    check_hip(hipMallocAsync(&p, nb, stream), "hipMallocAsync");
+    check(tq::zero_async(p, nb, stream), "workspace zero-fill");
+    if (w.ptr) check_hip(hipFreeAsync(w.ptr, stream), "hipFreeAsync");
+    w.ptr = p;
     w.bytes = nb;
   }
   *have = w.bytes;
@@ -158,10 +172,23 @@ void set_metallib_path(const std::string&) {}
 
 // ---------------------------------------------------------------------------
 
+size_t sdpa_int4_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                int max_kv_len) {
+  return tq_sdpa_int4_workspace_size(batch, num_heads, num_kv_heads, head_dim, max_kv_len);
+}
+
 void sdpa_int4_into(array& out, const array& queries, const array& k_quant, const array& k_scales,
                     const array& k_biases, const array& v_quant, const array& v_scales,
                     const array& v_biases, int gqa_factor, float scale, int sliding_window,
                     int kv_len, StreamOrDevice s) {
+  sdpa_int4_into(out, queries, k_quant, k_scales, k_biases, v_quant, v_scales, v_biases,
+                 gqa_factor, scale, sliding_window, kv_len, nullptr, 0, s);
+}
+
+void sdpa_int4_into(array& out, const array& queries, const array& k_quant, const array& k_scales,
+                    const array& k_biases, const array& v_quant, const array& v_scales,
+                    const array& v_biases, int gqa_factor, float scale, int sliding_window,
+                    int kv_len, void* workspace_ptr, size_t workspace_bytes, StreamOrDevice s) {
   need(queries.ndim() == 2, "queries must be (num_heads, head_dim)");
   need(k_quant.ndim() == 3 && v_quant.shape() == k_quant.shape(),
        "k_quant / v_quant must be (num_kv_heads, N, head_dim/8)");
@@ -175,8 +202,9 @@ void sdpa_int4_into(array& out, const array& queries, const array& k_quant, cons
   need(out.shape() == std::vector<int64_t>{Hq, D} && out.dtype() == Dtype::float32,
        "out must be (num_heads, head_dim) float32");
   const int n = kv_len < 0 ? cap : kv_len;
-  size_t have = 0;
-  void* ws = workspace(tq_sdpa_int4_workspace_size(1, Hq, Hkv, D, n), &have);
+  size_t have = workspace_bytes;
+  void* ws = workspace_ptr;
+  if (!ws) ws = workspace(tq_sdpa_int4_workspace_size(1, Hq, Hkv, D, n), &have, s);
   check(tq_sdpa_int4(queries.data(), c_dtype(queries.dtype()),
                      static_cast<const uint32_t*>(k_quant.data()), k_scales.data(),
                      k_biases.data(), static_cast<const uint32_t*>(v_quant.data()),
@@ -209,7 +237,7 @@ array sdpa_int4_ragged(const array& queries, const array& k_quant, const array& 
   need(is_sb(k_scales.dtype()), "scales must be float32 or float16");
   array out = array::empty({B, Hq, D}, Dtype::float32);
   size_t have = 0;
-  void* ws = workspace(tq_sdpa_int4_workspace_size(B, Hq, Hkv, D, cap), &have);
+  void* ws = workspace(tq_sdpa_int4_workspace_size(B, Hq, Hkv, D, cap), &have, s);
   check(tq_sdpa_int4_ragged(queries.data(), c_dtype(queries.dtype()),
                             static_cast<const uint32_t*>(k_quant.data()), k_scales.data(),
                             k_biases.data(), static_cast<const uint32_t*>(v_quant.data()),
@@ -235,7 +263,7 @@ array sdpa_int4_prefill(const array& queries, const array& k_quant, const array&
   need(is_sb(k_scales.dtype()), "scales must be float32 or float16");
   array out = array::empty({S, Hq, D}, Dtype::float32);
   size_t have = 0;
-  void* ws = workspace(tq_sdpa_int4_workspace_size(S > 0 ? S : 1, Hq, Hkv, D, n_prior + S), &have);
+  void* ws = workspace(tq_sdpa_int4_workspace_size(S > 0 ? S : 1, Hq, Hkv, D, n_prior + S), &have, s);
   check(tq_sdpa_int4_prefill(queries.data(), c_dtype(queries.dtype()),
                              static_cast<const uint32_t*>(k_quant.data()), k_scales.data(),
                              k_biases.data(), static_cast<const uint32_t*>(v_quant.data()),
@@ -463,7 +491,7 @@ array compressed_sdpa(const array& queries, const array& indices_l1, const array
   Codebooks cb = concat_codebooks(cb_l1, cb_l2, cb_l3, cb_l4, 1, s);
   array out = array::empty({Nq, D}, Dtype::float32);
   size_t have = 0;
-  void* ws = workspace(tq_compressed_sdpa_workspace_size(Nq, Nq, D, N), &have);
+  void* ws = workspace(tq_compressed_sdpa_workspace_size(Nq, Nq, D, N), &have, s);
   check(tq_compressed_sdpa(static_cast<const float*>(queries.data()), Nq,
                            static_cast<const uint8_t*>(indices_l1.data()),
                            static_cast<const uint8_t*>(indices_l2.data()),

@@ -219,11 +219,12 @@ def compressed_sdpa(queries, indices_l1, indices_l2, indices_l3, indices_l4, rad
     cb, sizes = _codebooks([cb_l1, cb_l2, cb_l3, cb_l4])
     out = torch.empty((Nq, D), dtype=torch.float32, device=queries.device)
     nbytes = _lib.load().tq_compressed_sdpa_workspace_size(Nq, Hkv, D, N)
-    ws = workspace(nbytes, queries.device)
+    sh = _stream(stream)
+    ws = workspace(nbytes, queries.device, sh)
     call("tq_compressed_sdpa", _ptr(queries), Nq, _ptr(indices_l1), _ptr(indices_l2),
          _ptr(indices_l3), _ptr(indices_l4), _ptr(radii), _ptr(cb), _sizes_ptr(sizes),
          _ptr(values), Hkv, N, D, int(block_size), float(scale), _ptr(out), _ptr(ws), ws.numel(),
-         _stream(stream))
+         sh)
     return out
 
 
@@ -344,8 +345,9 @@ class Polar7Codec:
         if out is None:
             out = torch.empty((Hq, P7_D), dtype=torch.float32, device=q_tables.device)
         nbytes = _lib.load().tq_polar7_sdpa_workspace_size(Hq, Hkv, n)
-        ws = workspace(nbytes, q_tables.device)
+        sh = _stream(stream)
+        ws = workspace(nbytes, q_tables.device, sh)
         call("tq_polar7_sdpa_int4v", _ptr(q_tables), _ptr(angles), _ptr(norms), _ptr(qjl),
              _ptr(self.cs), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out), Hq, Hkv,
-             n, cap, float(scale), int(sliding_window), _ptr(ws), ws.numel(), _stream(stream))
+             n, cap, float(scale), int(sliding_window), _ptr(ws), ws.numel(), sh)
         return out

@@ -6,8 +6,8 @@ device-memory / stream plumbing -- every computation runs in
 ``libturboquant_hip.so`` through the C ABI, see ``_lib.py``).
 
 Like the reference's ``eval_gpu`` (``lib/turboquant.cpp:372``) these wrappers
-allocate their outputs; the split-K workspace is a zero-filled per-device
-buffer grown on demand and reused (the kernels leave it zeroed).
+allocate their outputs; the split-K workspace is a zero-filled buffer per
+(device, stream), grown on demand and reused (the kernels leave it zeroed).
 """
 from __future__ import annotations
 
@@ -61,12 +61,23 @@ def _sb_dtype(name: str, t: torch.Tensor) -> int:
     return _DT[t.dtype]
 
 
-def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """Zero-initialised scratch of at least ``nbytes`` on ``device`` (cached)."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
+def workspace(nbytes: int, device: torch.device, stream_handle: int) -> torch.Tensor:
+    """Zero-initialised split-K scratch of at least ``nbytes`` for calls on
+    one (device, stream) (cached).  Calls on one stream run in order and share
+    it; calls on different streams never do.  A new or grown buffer is
+    allocated and zero-filled on that stream (torch's allocator then orders
+    its reuse after the stream's queued work), so the fill is ordered before
+    the kernels that use it, and a replaced buffer is released only behind
+    the calls already queued there.  The first call on a (device, stream)
+    must not be under graph capture (tq_sdpa_int4_noalloc serves such
+    callers)."""
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    key = (dev, stream_handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        s = torch.cuda.ExternalStream(stream_handle, device=torch.device("cuda", dev))
+        with torch.cuda.stream(s):
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 
@@ -117,11 +128,12 @@ def sdpa_int4(queries: torch.Tensor,
         _check_cuda("out", out)
         _need(out.shape == (Hq, D) and out.dtype == torch.float32, "out must be (Hq, D) float32")
     nbytes = _decode_ws_size(Hq, Hkv, D, n)
-    ws = workspace(nbytes, queries.device)
+    sh = _stream(stream)
+    ws = workspace(nbytes, queries.device, sh)
     call("tq_sdpa_int4", queries.data_ptr(), qdt, k_quant.data_ptr(), k_scales.data_ptr(),
          k_biases.data_ptr(), v_quant.data_ptr(), v_scales.data_ptr(), v_biases.data_ptr(), sbt,
          out.data_ptr(), Hq, Hkv, D, n, cap, int(gqa_factor), float(scale), int(sliding_window),
-         ws.data_ptr(), ws.numel(), _stream(stream))
+         ws.data_ptr(), ws.numel(), sh)
     return out
 
 
@@ -189,11 +201,12 @@ def sdpa_int4_prefill(queries: torch.Tensor,
     _check_cuda("out", out)
     _need(out.shape == (S, Hq, D) and out.dtype == torch.float32, "out must be (n_new, Hq, D) f32")
     nbytes = _lib.load().tq_sdpa_int4_workspace_size(max(S, 1), Hq, Hkv, D, int(n_prior) + S)
-    ws = workspace(nbytes, queries.device)
+    sh = _stream(stream)
+    ws = workspace(nbytes, queries.device, sh)
     call("tq_sdpa_int4_prefill", _ptr(queries), _DT[queries.dtype], _ptr(k_quant), _ptr(k_scales),
          _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out), Hq, Hkv,
          D, int(n_prior), S, cap, int(gqa_factor), float(scale), int(sliding_window), _ptr(ws),
-         ws.numel(), _stream(stream))
+         ws.numel(), sh)
     return out
 
 
@@ -232,11 +245,12 @@ def sdpa_int4_ragged(queries: torch.Tensor,
     if out is None:
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
     nbytes = _lib.load().tq_sdpa_int4_workspace_size(B, Hq, Hkv, D, mx)
-    ws = workspace(nbytes, queries.device)
+    sh = _stream(stream)
+    ws = workspace(nbytes, queries.device, sh)
     call("tq_sdpa_int4_ragged", _ptr(queries), _DT[queries.dtype], _ptr(k_quant),
          _ptr(k_scales), _ptr(k_biases), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt,
          _ptr(out), B, Hq, Hkv, D, cap, _ptr(seq_lens), _ptr(windows), mx, int(gqa_factor),
-         float(scale), int(sliding_window), _ptr(ws), ws.numel(), _stream(stream))
+         float(scale), int(sliding_window), _ptr(ws), ws.numel(), sh)
     return out
 
 

@@ -75,12 +75,27 @@ array sdpa_int4(const array& queries, const array& k_quant, const array& k_scale
                 int sliding_window = 0, StreamOrDevice s = {});
 
 // The same into a caller-owned output, over rows [0, kv_len) of caches whose
-// row stride is k_quant.shape(1) (kv_len < 0: all rows).
+// row stride is k_quant.shape(1) (kv_len < 0: all rows).  The split-K
+// workspace is the library's buffer for the calling (device, stream).
 void sdpa_int4_into(array& out, const array& queries, const array& k_quant,
                     const array& k_scales, const array& k_biases, const array& v_quant,
                     const array& v_scales, const array& v_biases, int gqa_factor,
                     float scale = 1.0f, int sliding_window = 0, int kv_len = -1,
                     StreamOrDevice s = {});
+
+// The same with a caller-owned split-K workspace of workspace_bytes (at
+// least sdpa_int4_workspace_size(1, ...), zero-filled once before first use;
+// the kernels leave it zeroed).  Calls that may run concurrently need
+// separate workspaces.  Allocates nothing.
+void sdpa_int4_into(array& out, const array& queries, const array& k_quant,
+                    const array& k_scales, const array& k_biases, const array& v_quant,
+                    const array& v_scales, const array& v_biases, int gqa_factor, float scale,
+                    int sliding_window, int kv_len, void* workspace, size_t workspace_bytes,
+                    StreamOrDevice s = {});
+
+// Workspace bytes of a decode call (tq_sdpa_int4_workspace_size).
+size_t sdpa_int4_workspace_size(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                int max_kv_len);
 
 // Batched ragged decode: queries (B, num_heads, head_dim), caches (B,
 // num_kv_heads, capacity, .), seq_lens / windows int32 (B) device arrays

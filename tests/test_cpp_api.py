@@ -10,6 +10,7 @@ LIB = os.path.join(ROOT, "gemma4metal_amd", "libturboquant_hip.so")
 EXE = os.path.join(ROOT, "tests", "cpp", "test_sdpa_int4")
 
 CXX_API = ["turboquant::sdpa_int4(", "turboquant::sdpa_int4_into(", "turboquant::sdpa_int4_ragged(",
+           "turboquant::sdpa_int4_workspace_size(",
            "turboquant::quantize(", "turboquant::dequantize(", "turboquant::kv_append_int4(",
            "turboquant::polar_quantize(", "turboquant::polar_dequantize(",
            "turboquant::polar_quantize_packed(", "turboquant::polar_dequantize_packed(",
@@ -36,4 +37,4 @@ def test_cxx_sdpa_int4_matches_reference_composition():
     r = subprocess.run([EXE], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.count("PASS") == 5
+    assert r.stdout.count("PASS") == 6

@@ -489,3 +489,35 @@ def test_sdpa_prefill_tile_and_split_paths_agree(gpu, tq_env):
     tq_env("TQ_PREFILL_IMPL", "splitk")
     split = host(gpu.sdpa_int4_prefill(qd, *cd, prior, 2, 1.0, W))
     assert np.abs(tiles - split).max() < 1e-3
+
+
+def test_fresh_workspace_on_non_default_streams(gpu):
+    """Calls on non-default streams, each getting a fresh workspace on its
+    first call: the zero-fill is ordered on the call's stream, and two
+    streams never share counters.  Decode and ragged, interleaved on two
+    streams without synchronisation between them, match the default-stream
+    results bit for bit."""
+    rng = np.random.default_rng(515)
+    Hq, Hkv, D, L = 32, 16, 256, 9000
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    cd = [dev(a) for a in host_cache(rng, Hkv, L, D)]
+    B, cap = 3, 2000
+    lens = np.array([2000, 17, 1500], np.int32)
+    qr, _ = queries(rng, (B, Hq, D), "bf16")
+    k = O.rms_norm(rng.standard_normal((B, Hkv, cap, D)).astype(np.float32))
+    v = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    cr = [dev(a) for a in (O.quantize_int4(k) + O.quantize_int4(v))]
+    ld = dev(lens)
+    ref_d = host(gpu.sdpa_int4(qd, *cd, 2))
+    ref_r = host(gpu.sdpa_int4_ragged(qr, *cr, ld, 2))
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for rep in range(4):
+        for s in (s1, s2):
+            with torch.cuda.stream(s):
+                outs.append(("d", gpu.sdpa_int4(qd, *cd, 2, stream=s)))
+                outs.append(("r", gpu.sdpa_int4_ragged(qr, *cr, ld, 2, stream=s)))
+    torch.cuda.synchronize()
+    for kind, o in outs:
+        assert np.array_equal(host(o), ref_d if kind == "d" else ref_r), kind
