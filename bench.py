@@ -52,26 +52,38 @@ def parse():
                     choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar", "global",
                              "prefill"])
     ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--sb", default="f16", choices=["f16", "f32"],
+                    help="K/V scale/bias dtype: f16 (BASELINE) or f32 (the reference's cache)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--out", default=None, help="also append the JSON line to this file")
     return ap.parse_args()
 
 
-def gen_cache(tq, torch, Hkv, L, D, gen, cap=None):
-    """One int4 KV set built on the GPU: RMS-normed N(0,1) K, N(0,1) V."""
+def gen_cache(tq, torch, Hkv, L, D, gen, cap=None, sb=None):
+    """One int4 KV set built on the GPU: RMS-normed N(0,1) K, N(0,1) V,
+    scale/bias in `sb` (default fp16)."""
     cap = cap or L
+    sb = sb or torch.float16
     kq = torch.empty((Hkv, cap, D // 8), dtype=torch.uint32, device="cuda")
     vq = torch.empty_like(kq)
-    ks = torch.empty((Hkv, cap, D // 64), dtype=torch.float16, device="cuda")
+    ks = torch.empty((Hkv, cap, D // 64), dtype=sb, device="cuda")
     kb, vs, vb = torch.empty_like(ks), torch.empty_like(ks), torch.empty_like(ks)
     for h in range(Hkv):
         k = torch.randn((cap, D), generator=gen, device="cuda")
         k = k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)
         v = torch.randn((cap, D), generator=gen, device="cuda")
-        kq[h], ks[h], kb[h] = tq.quantize(k, scale_dtype=torch.float16)
-        vq[h], vs[h], vb[h] = tq.quantize(v, scale_dtype=torch.float16)
+        kq[h], ks[h], kb[h] = tq.quantize(k, scale_dtype=sb)
+        vq[h], vs[h], vb[h] = tq.quantize(v, scale_dtype=sb)
     return kq, ks, kb, vq, vs, vb
+
+
+def precision_note(sb_name):
+    """The arithmetic of the matrix-core decode kernel, stated in full."""
+    return (f"int4 K/V ({sb_name} scale/bias), bf16 Q; K.q on int8 matrix cores with q as "
+            "22-bit fixed point per head (exact integer dot per quant group), P.V on bf16 "
+            "matrix cores with the weights p*s_v split into bf16 hi+lo (~16-bit mantissa), "
+            "fp32 accumulate and softmax")
 
 
 def gen_q(torch, shape, gen):
@@ -162,15 +174,19 @@ def main():
     gen = torch.Generator(device="cuda").manual_seed(2026)
     res = {}
 
+    sbt = torch.float32 if args.sb == "f32" else torch.float16
+    sb_bytes = 4 if args.sb == "f32" else 2
     if args.workload in ("ctx32k", "sweep"):
         lens = [args.ctx] if args.workload == "ctx32k" else [1024, 8192, 32768, 131072, 262144]
         lines = []
         for L in lens:
-            nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkv * L * 288)))
-            sets = [gen_cache(tq, torch, Hkv, L, D, gen) for _ in range(nsets)]
+            row = O.row_bytes(D, sb_bytes)
+            nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkv * L * row)))
+            sets = [gen_cache(tq, torch, Hkv, L, D, gen, sb=sbt) for _ in range(nsets)]
             qs = [gen_q(torch, (Hq, D), gen) for _ in range(nsets)]
             out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
-            nbytes = O.decode_bytes(Hq, Hkv, D, L)
+            nbytes = O.decode_bytes(Hq, Hkv, D, L, sb_bytes=sb_bytes)
+            plan = tq.sdpa_plan(Hq, Hkv, D, L, sb_dtype=sbt)
 
             def step(i):
                 s = i % nsets
@@ -185,23 +201,30 @@ def main():
                 "ms_per_step": round(ms_step, 5), "us_per_layer": round(ms_step * 1e3, 2),
                 "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-                "dtype": "int4 K/V (fp16 scale/bias), bf16 Q, fp32 accumulate",
+                "dtype": precision_note(args.sb),
                 "data": "synthetic (seeded N(0,1), RMS-normed Q/K), random-init; "
                         f"{nsets} rotated KV sets",
                 "config": {"workload": f"sdpa_int4 decode layer Hq={Hq} Hkv={Hkv} D={D} "
-                                       f"L={L} W=0 (BASELINE configs[2])",
+                                       f"L={L} W=0, {args.sb} scale/bias (BASELINE configs[2])",
                            "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"},
                 # the timed region is back-to-back launches of this one kernel
                 # on one stream, so region time / K is its mean launch time
                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_GBS,
                              "unit": "GB/s", "frac": round(gbs / PEAK_GBS, 4),
-                             "traffic": measured_traffic() if L == 32768 else None,
-                             "kernel": "sdpa_int4_mfma_kernel<256,2,8,false,true>",
+                             "kernel": plan["kernel"], "splits": plan["splits"],
+                             "keys_per_split": plan["chunk"],
                              "bytes_per_launch": nbytes,
                              "us_per_launch": round(ms_step * 1e3, 2),
                              "us_per_launch_event_bracketed_mean": round(ms_launch * 1e3, 2),
                              "us_per_launch_event_bracketed_median": round(ms_med * 1e3, 2)},
             }
+            # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+            # passes committed for this exact launch (headline shape, fp16
+            # scale/bias); not measured by this run
+            traffic = measured_traffic() if (L == 32768 and args.sb == "f16") else None
+            line["roofline"]["traffic"] = traffic
+            if traffic is not None:
+                line["roofline"]["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
             if not args.no_cpu and L == lens[0]:
                 s0 = sets[0]
                 host = []
@@ -256,11 +279,12 @@ def main():
         # Gemma global-attention layer shape (engine/gemma4_multilayer.cpp:3,49-51):
         # Hq 32, Hkv 4 (GQA 8), D 512, no window
         Hg, Hkvg, Dg, L = 32, 4, 512, args.ctx
-        nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkvg * L * 576)))
-        sets = [gen_cache(tq, torch, Hkvg, L, Dg, gen) for _ in range(nsets)]
+        nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkvg * L * O.row_bytes(Dg, sb_bytes))))
+        sets = [gen_cache(tq, torch, Hkvg, L, Dg, gen, sb=sbt) for _ in range(nsets)]
         qs = [gen_q(torch, (Hg, Dg), gen) for _ in range(nsets)]
         out = torch.empty((Hg, Dg), dtype=torch.float32, device="cuda")
-        nbytes = O.decode_bytes(Hg, Hkvg, Dg, L)
+        nbytes = O.decode_bytes(Hg, Hkvg, Dg, L, sb_bytes=sb_bytes)
+        plan = tq.sdpa_plan(Hg, Hkvg, Dg, L, sb_dtype=sbt)
         ms_step, _, _ = time_launches(torch, lambda i: tq.sdpa_int4(
             qs[i % nsets], *sets[i % nsets], Hg // Hkvg, 1.0, 0, out=out), args.steps, args.warmup)
         gbs = nbytes / (ms_step * 1e-3) / 1e9
@@ -269,17 +293,19 @@ def main():
               "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
               "us_per_layer": round(ms_step * 1e3, 2), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-              "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
-              "config": {"workload": f"sdpa_int4 Hq={Hg} Hkv={Hkvg} D={Dg} L={L} W=0 (global layer)",
+              "dtype": precision_note(args.sb), "data": "synthetic",
+              "kernel": plan["kernel"], "splits": plan["splits"],
+              "config": {"workload": f"sdpa_int4 Hq={Hg} Hkv={Hkvg} D={Dg} L={L} W=0, {args.sb} "
+                                     "scale/bias (global layer)",
                          "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"}}, args)
         return
 
     if args.workload == "sliding50":
         L, W, layers = 786, 1024, 50
-        sets = [gen_cache(tq, torch, Hkv, L, D, gen) for _ in range(layers)]
+        sets = [gen_cache(tq, torch, Hkv, L, D, gen, sb=sbt) for _ in range(layers)]
         q = gen_q(torch, (Hq, D), gen)
         out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
-        nbytes = O.decode_bytes(Hq, Hkv, D, L)
+        nbytes = O.decode_bytes(Hq, Hkv, D, L, sb_bytes=sb_bytes)
 
         def one_step():
             for s in sets:
@@ -297,9 +323,10 @@ def main():
               "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
               "us_per_layer": round(us_layer, 3), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-              "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
-              "config": {"workload": "50 x sdpa_int4 Hq=32 Hkv=16 D=256 L=786 W=1024 "
-                                     "(BASELINE configs[1]), one HIP graph per step",
+              "dtype": precision_note(args.sb), "data": "synthetic",
+              "config": {"workload": "50 x sdpa_int4 Hq=32 Hkv=16 D=256 L=786 W=1024, "
+                                     f"{args.sb} scale/bias (BASELINE configs[1]), one HIP graph "
+                                     "per step",
                          "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"}},
              args)
         return

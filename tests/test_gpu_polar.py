@@ -254,7 +254,9 @@ def host_norms(n):
 
 
 @pytest.mark.parametrize("Hq,Hkv,L,scale", [(32, 16, 2000, 1.0), (4, 4, 333, 0.3), (16, 2, 1200, 1.0),
-                                            (8, 8, 70, 1.0)])
+                                            (8, 8, 70, 1.0),
+                                            (32, 16, 5000, 1.0),   # 3 blocks of 2048, partial last
+                                            (8, 2, 4096, 0.5)])    # exactly two blocks
 def test_polar7_score(pq, Hq, Hkv, L, scale):
     rng, codec, P, S, dk, hk, _ = p7_cache_on_gpu(pq, Hq + L, Hkv, L)
     q = rng.standard_normal((Hq, 128)).astype(f32)
@@ -308,3 +310,20 @@ def test_polar7_full_size_two_heads(pq):
         ref = PQ.polar7_sdpa_int4v(hqp[2 * kvh:2 * kvh + 2], hqs[2 * kvh:2 * kvh + 2], hk[0][sl],
                                    host_norms(hk[1][sl]), hk[2][sl], vq[sl], vs[sl], vb[sl], 2)
         assert_close(got[2 * kvh:2 * kvh + 2], ref, f"kv head {kvh}")
+
+
+def test_polar7_score_full_size_two_heads(pq):
+    """The score-only launch at the configs[4] shape (Hq 32, Hkv 16,
+    L 32768: 16 blocks of 2048 keys per head), checked on two kv heads."""
+    Hq, Hkv, L = 32, 16, 32768
+    rng, codec, P, S, dk, hk, _ = p7_cache_on_gpu(pq, 4242, Hkv, L)
+    q = rng.standard_normal((Hq, 128)).astype(f32)
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    got = host(codec.score(tab, *dk))
+    hqp, hqs = host(qp), host(qs)
+    for kvh in (0, 13):
+        sl = slice(kvh, kvh + 1)
+        ref = PQ.polar7_scores(hqp[2 * kvh:2 * kvh + 2], hqs[2 * kvh:2 * kvh + 2], hk[0][sl],
+                               host_norms(hk[1][sl]), hk[2][sl], 2)
+        err = np.abs(got[2 * kvh:2 * kvh + 2] - ref)
+        assert err.max() < SCORE_ATOL, f"kv head {kvh}: max score err {err.max():.3e}"
