@@ -552,7 +552,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
       // 8 heads x 512 dims of partials per split: merged by a separate,
       // parallel kernel rather than one workgroup per kv head
       p.ext_merge = max_splits > 1 ? 1 : 0;
-      const int r = launch_sdpa_hc(p, grid, s);
+      const int r = launch_sdpa_hc(p, sb_dtype, grid, s);
       if (r != TQ_OK || !p.ext_merge) return r;
       return launch_merge_splits(p, D, batch, s);
     }

@@ -380,7 +380,7 @@ int launch_sdpa_mfma(const SdpaParams& p, int D, int G, int sb_dtype, dim3 grid,
                      hipStream_t stream);
 // D = 512, 8 query heads per workgroup (heads as matrix-core columns), fp16
 // scale/bias: tq_sdpa_hc.hip.
-int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t stream);
+int launch_sdpa_hc(const SdpaParams& p, int sb_dtype, dim3 grid, hipStream_t stream);
 // Prefill with K/V tiles shared by 64 (query, head) rows (tq_prefill.hip);
 // -1 when the shape is not served (D other than 128 / 256, fp32 scales,
 // gqa not dividing 64).

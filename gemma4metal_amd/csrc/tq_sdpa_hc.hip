@@ -55,16 +55,14 @@ constexpr int kHcRB = 256; // bytes per packed row
 struct HcBuf {
   uint32_t kw[2][16];  // [tile][4 P + 2 h + e]: word 8 (2P + c/2) + 4h + 2 (c%2) + e of key 16 tile + m
   uint32_t vw[8][4];   // [slot][blk]: word 16 blk + m of the slot's key
-  uint32_t sc[2][4];   // scales of array c for keys 2m, 2m+1 (8 fp16 each)
+  u32x4 sc[2][1];      // scales of array c for keys 2m, 2m+1 (8 fp16 each)
 };
 
 // Loads of the 32 keys at t0 (rows clamped to `last`, the uniform limit
 // `lim` = last - t0 >= 0), non-temporal, uniform base + 32-bit lane offset:
-// K words and the scale arrays, and the V words, as separate parts.
-__device__ __forceinline__ void hc_load_k(uint32_t (&kw)[2][16], uint32_t (&scw)[2][4], const char* kq,
-                                          const char* sc, int t0, int lim, int m, int c) {
+// K words, the scale arrays and the V words, as separate parts.
+__device__ __forceinline__ void hc_load_kw(uint32_t (&kw)[2][16], const char* kq, int t0, int lim, int m, int c) {
   const char* kb = kq + static_cast<int64_t>(t0) * kHcRB;
-  const char* sb = sc + static_cast<int64_t>(t0) * 16;
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
     // lane group c takes group 2P + c / 2 of each pair, dims 16 (c % 2) ..
@@ -77,12 +75,28 @@ __device__ __forceinline__ void hc_load_k(uint32_t (&kw)[2][16], uint32_t (&scw)
       kw[tile][2 * j + 1] = u.y;
     }
   }
+}
+
+// Scale array of lane group c (k scale, k bias, v scale, v bias) for keys
+// 2m, 2m + 1: 8 groups per key, fp16 (4 words per key) or fp32 (8 words).
+template <bool F32>
+__device__ __forceinline__ void hc_load_sc(u32x4 (&scw)[2][F32 ? 2 : 1], const char* sc, int t0, int lim,
+                                           int m) {
+  constexpr int RB = F32 ? 32 : 16;  // scale bytes per key
+  const char* sb = sc + static_cast<int64_t>(t0) * RB;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const uint32_t off = static_cast<uint32_t>(min(2 * m + e, lim)) * 16;
-    const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sb + off));
-    scw[e][0] = u.x; scw[e][1] = u.y; scw[e][2] = u.z; scw[e][3] = u.w;
+    const uint32_t off = static_cast<uint32_t>(min(2 * m + e, lim)) * RB;
+#pragma unroll
+    for (int h = 0; h < RB / 16; ++h)
+      scw[e][h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(sb + off + 16 * h));
   }
+}
+
+__device__ __forceinline__ void hc_load_k(uint32_t (&kw)[2][16], u32x4 (&scw)[2][1], const char* kq,
+                                          const char* sc, int t0, int lim, int m, int c) {
+  hc_load_kw(kw, kq, t0, lim, m, c);
+  hc_load_sc<false>(scw, sc, t0, lim, m);
 }
 
 __device__ __forceinline__ void hc_load_v(uint32_t (&vw)[8][4], const char* vq, int t0, int lim, int m,
@@ -288,7 +302,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
     // scales -> LDS [array][group][key pair]
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      const uint32_t a0 = B.sc[0][g >> 1], a1 = B.sc[1][g >> 1];
+      const uint32_t a0 = B.sc[0][0][g >> 1], a1 = B.sc[1][0][g >> 1];
       sc_lds[wv][c][g][m] = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u)) : ((a0 & 0xFFFFu) | (a1 << 16));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -491,6 +505,9 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
 // SIMD.
 constexpr int kHs = 4;  // key streams (producer / consumer pairs)
 
+// F32: fp32 scale/bias (8 words per key in each array instead of 4); the
+// producer's scale registers and LDS stage double, nothing else changes.
+template <bool F32>
 __global__ __launch_bounds__(2 * kHs * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_int4_hc2_kernel(SdpaParams p) {
   pin_args(p);
@@ -517,7 +534,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   __shared__ __attribute__((aligned(16))) float arena[kArenaWords];
   uint4* pv_lds = reinterpret_cast<uint4*>(arena);
   __shared__ uint4 bq_lds[3][NG][64];         // K MFMA B operands [digit][2 pair + half][lane]
-  __shared__ uint32_t sc_lds[NS][4][NG][16];  // [stream][array][group][key pair] fp16 x 2
+  // [stream][array][group][key pair] fp16 x 2, or [..][key] fp32
+  constexpr int SK = F32 ? 32 : 16;
+  __shared__ __attribute__((aligned(16))) uint32_t sc_lds[NS][4][NG][SK];
   __shared__ float f_lds[2][NS][16];          // rescale factor per column, by slot
   __shared__ float off_lds[NS][4][16];        // final offset per (block, column)
   __shared__ float red_max[NE][NWV];
@@ -528,7 +547,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   const char* kq_rows = reinterpret_cast<const char*>(p.kq + row0 * (D / 8));
   const char* vq_rows = reinterpret_cast<const char*>(p.vq + row0 * (D / 8));
   const void* sc_base = c == 0 ? p.ks : (c == 1 ? p.kb : (c == 2 ? p.vs : p.vb));
-  const char* sc_rows = static_cast<const char*>(sc_base) + row0 * 16;
+  const char* sc_rows = static_cast<const char*>(sc_base) + row0 * (F32 ? 32 : 16);
 
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const bool producer = wv < NS;
@@ -574,8 +593,15 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     uint32_t qraw[NE];
     load_q(qraw);
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t kA[2][16], kB[2][16], sA[2][4], sB[2][4];
-    hc_load_k(kA, sA, kq_rows, sc_rows, tclamp(base0), safe_last - tclamp(base0), m, c);
+    constexpr int SW = F32 ? 2 : 1;  // 16-byte scale vectors per key
+    uint32_t kA[2][16], kB[2][16];
+    u32x4 sA[2][SW], sB[2][SW];
+    auto load_k = [&](uint32_t (&kw)[2][16], u32x4 (&scw)[2][SW], int t0) {
+      const int tc = tclamp(t0);
+      hc_load_kw(kw, kq_rows, tc, safe_last - tc, m, c);
+      hc_load_sc<F32>(scw, sc_rows, tc, safe_last - tc, m);
+    };
+    load_k(kA, sA, base0);
     __builtin_amdgcn_sched_barrier(0);
     q_image(qraw);
     const float sf = ldexpf(1.0f, -sh_F[hh]);
@@ -588,14 +614,28 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) wsum[blk] = bacc[blk] = 0.0f;
 
-    auto produce = [&](const uint32_t (&kw)[2][16], const uint32_t (&scw)[2][4], int st) {
+    auto produce = [&](const uint32_t (&kw)[2][16], const u32x4 (&scw)[2][SW], int st) {
       const int t0 = base0 + st * kIter, slot = st & 1;
-      // scales -> LDS [array][group][key pair]
+      // scales -> LDS [array][group][key pair] (fp16) or [..][key] (fp32)
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
-        const uint32_t a0 = scw[0][g >> 1], a1 = scw[1][g >> 1];
-        sc_lds[s][c][g][m] = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u)) : ((a0 & 0xFFFFu) | (a1 << 16));
+        if constexpr (F32) {
+          *reinterpret_cast<u32x2*>(&sc_lds[s][c][g][2 * m]) = u32x2{scw[0][g >> 2][g & 3], scw[1][g >> 2][g & 3]};
+        } else {
+          const uint32_t a0 = scw[0][0][g >> 1], a1 = scw[1][0][g >> 1];
+          sc_lds[s][c][g][m] = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u)) : ((a0 & 0xFFFFu) | (a1 << 16));
+        }
       }
+      // the scale arrays' entries of keys k0 .. k0 + 3 (k0 % 4 == 0) of
+      // group g, as fp32
+      auto scale4 = [&](int a, int g, int k0) -> v4f {
+        if constexpr (F32) {
+          return *reinterpret_cast<const v4f*>(&sc_lds[s][a][g][k0]);
+        } else {
+          const uint2 u = *reinterpret_cast<const uint2*>(&sc_lds[s][a][g][k0 >> 1]);
+          return v4f{hc_half(u.x, 0), hc_half(u.x, 1), hc_half(u.y, 0), hc_half(u.y, 1)};
+        }
+      };
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -630,13 +670,11 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
           acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b01, acc0, 0, 0, 0);
           acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b11, acc1, 0, 0, 0);
           acc2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b21, acc2, 0, 0, 0);
-          const uint2 ks = *reinterpret_cast<const uint2*>(&sc_lds[s][0][gl][8 * tile + 2 * c]);
-          const uint2 kb = *reinterpret_cast<const uint2*>(&sc_lds[s][1][gl][8 * tile + 2 * c]);
+          const v4f ks = scale4(0, gl, 16 * tile + 4 * c), kb = scale4(1, gl, 16 * tile + 4 * c);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float dot = static_cast<float>((acc2[i] << 16) + ((acc1[i] << 8) + acc0[i]));
-            const uint32_t ksw = (i >> 1) ? ks.y : ks.x, kbw = (i >> 1) ? kb.y : kb.x;
-            sc[tile][i] = fmaf(dot, hc_half(ksw, i & 1), fmaf(hc_half(kbw, i & 1), qh[P], sc[tile][i]));
+            sc[tile][i] = fmaf(dot, ks[i], fmaf(kb[i], qh[P], sc[tile][i]));
           }
         }
       }
@@ -681,21 +719,18 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         const int gv = 2 * blk + (m >> 3);
-        const uint2 vs0 = *reinterpret_cast<const uint2*>(&sc_lds[s][2][gv][2 * c]);
-        const uint2 vs1 = *reinterpret_cast<const uint2*>(&sc_lds[s][2][gv][8 + 2 * c]);
-        const uint2 vb0 = *reinterpret_cast<const uint2*>(&sc_lds[s][3][gv][2 * c]);
-        const uint2 vb1 = *reinterpret_cast<const uint2*>(&sc_lds[s][3][gv][8 + 2 * c]);
-        const uint32_t vsw[4] = {vs0.x, vs0.y, vs1.x, vs1.y};
-        const uint32_t vbw[4] = {vb0.x, vb0.y, vb1.x, vb1.y};
+        // slot j: key 16 (j / 4) + 4c + j % 4
+        const v4f vs[2] = {scale4(2, gv, 4 * c), scale4(2, gv, 16 + 4 * c)};
+        const v4f vb[2] = {scale4(3, gv, 4 * c), scale4(3, gv, 16 + 4 * c)};
         __bf16 hi[8], lo[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float w = pw[j] * hc_half(vsw[j >> 1], j & 1);
+          const float w = pw[j] * vs[j >> 2][j & 3];
           hi[j] = static_cast<__bf16>(w);
           const float hf = static_cast<float>(hi[j]);
           lo[j] = static_cast<__bf16>(w - hf);
           wsum[blk] += hf + static_cast<float>(lo[j]);
-          bacc[blk] = fmaf(pw[j], hc_half(vbw[j >> 1], j & 1), bacc[blk]);
+          bacc[blk] = fmaf(pw[j], vb[j >> 2][j & 3], bacc[blk]);
         }
         const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
         const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
@@ -706,13 +741,11 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     };
 
     for (int st = 0; st < NI; st += 2) {
-      hc_load_k(kB, sB, kq_rows, sc_rows, tclamp(base0 + (st + 1) * kIter),
-                safe_last - tclamp(base0 + (st + 1) * kIter), m, c);
+      load_k(kB, sB, base0 + (st + 1) * kIter);
       __builtin_amdgcn_sched_barrier(0);
       produce(kA, sA, st);
       __syncthreads();
-      hc_load_k(kA, sA, kq_rows, sc_rows, tclamp(base0 + (st + 2) * kIter),
-                safe_last - tclamp(base0 + (st + 2) * kIter), m, c);
+      load_k(kA, sA, base0 + (st + 2) * kIter);
       __builtin_amdgcn_sched_barrier(0);
       produce(kB, sB, st + 1);
       __syncthreads();
@@ -902,17 +935,26 @@ int launch_merge_splits(const SdpaParams& p, int D, int batch, hipStream_t s) {
   return TQ_OK;
 }
 
-bool hc_serves(int sb_dtype) { return sb_dtype == TQ_F16; }
+// fp16 scale/bias on either kernel; fp32 on the wave-specialised one
+bool hc_serves(int sb_dtype) {
+  return sb_dtype == TQ_F16 || (sb_dtype == TQ_F32 && !options().hc_one);
+}
 
-int launch_sdpa_hc(const SdpaParams& p, dim3 grid, hipStream_t s) {
-  // TQ_HC_IMPL=1 selects the one-wave-per-SIMD kernel
-  const bool one = options().hc_one;
-  if (one) {
+int launch_sdpa_hc(const SdpaParams& p, int sb_dtype, dim3 grid, hipStream_t s) {
+  // TQ_HC_IMPL=1 selects the one-wave-per-SIMD kernel (fp16 scale/bias)
+  if (!hc_serves(sb_dtype)) {
+    set_error("sdpa_int4: the heads-as-columns kernel does not serve this scale/bias dtype");
+    return TQ_ERR_INVALID;
+  }
+  if (options().hc_one) {
     sdpa_int4_hc_kernel<<<grid, kHcWaves * 64, 0, s>>>(p);
     TQ_CHECK_LAUNCH("sdpa_int4_hc_kernel");
+  } else if (sb_dtype == TQ_F32) {
+    sdpa_int4_hc2_kernel<true><<<grid, 2 * kHs * 64, 0, s>>>(p);
+    TQ_CHECK_LAUNCH("sdpa_int4_hc2_kernel<true>");
   } else {
-    sdpa_int4_hc2_kernel<<<grid, 2 * kHs * 64, 0, s>>>(p);
-    TQ_CHECK_LAUNCH("sdpa_int4_hc2_kernel");
+    sdpa_int4_hc2_kernel<false><<<grid, 2 * kHs * 64, 0, s>>>(p);
+    TQ_CHECK_LAUNCH("sdpa_int4_hc2_kernel<false>");
   }
   return TQ_OK;
 }

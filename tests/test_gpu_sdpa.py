@@ -43,7 +43,7 @@ def test_sdpa_matches_oracle(gpu, Hq, Hkv, D, L, W, qdt, sb, scale):
     (32, 16, 256, 1500, 1024), # window active
     (2, 1, 128, 33, 0),        # the reference test shape
     (32, 4, 256, 1500, 0),     # GQA 8 at D 256: two 4-head subgroups per kv head
-    (32, 4, 512, 2000, 0),     # Gemma global layer with fp32 scales: 2-head subgroups
+    (12, 4, 512, 2000, 0),     # D 512, GQA 3: one-head subgroups
     (8, 8, 512, 700, 0),       # D 512, GQA 1
     (16, 2, 128, 2100, 0),     # D 128, GQA 8: all 16 columns
 ])
@@ -201,6 +201,41 @@ def test_sdpa_d512_gqa8(gpu, Hq, Hkv, L, W, qdt):
     out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv, 1.0, W)
     ref = O.sdpa_int4(qv, *c, Hq // Hkv, 1.0, W)
     assert_close(host(out), ref, f"D512 Hq{Hq} Hkv{Hkv} L{L} W{W}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,W,qdt", [
+    (32, 4, 5000, 0, "bf16"),     # Gemma global layer, fp32 scale/bias (the reference's cache)
+    (32, 4, 3001, 1024, "bf16"),  # window active
+    (32, 2, 2100, 0, "f16"),      # GQA 16: two 8-head subgroups per kv head
+    (8, 1, 1, 0, "f32"),          # single key
+    (16, 2, 129, 0, "bf16"),      # one split, odd step count
+    (16, 2, 257, 0, "bf16"),
+])
+def test_sdpa_d512_gqa8_f32_scales(gpu, Hq, Hkv, L, W, qdt):
+    """fp32 scale/bias (lib/turboquant.h:199) on the wave-specialised
+    heads-as-columns kernel."""
+    assert gpu.sdpa_plan(Hq, Hkv, 512, L, sb_dtype=torch.float32,
+                         sliding_window=W)["kernel"] == "sdpa_int4_hc2_kernel"
+    rng = np.random.default_rng(Hq * 113 + L * 5 + W)
+    qd, qv = queries(rng, (Hq, 512), qdt)
+    c = host_cache(rng, Hkv, L, 512, "f32")
+    out = gpu.sdpa_int4(qd, *[dev(a) for a in c], Hq // Hkv, 1.0, W)
+    ref = O.sdpa_int4(qv, *c, Hq // Hkv, 1.0, W)
+    assert_close(host(out), ref, f"f32 s/b D512 Hq{Hq} Hkv{Hkv} L{L} W{W}")
+
+
+def test_sdpa_d512_gqa8_f32_scales_ragged(gpu):
+    rng = np.random.default_rng(52)
+    B, Hq, Hkv, D, cap = 3, 32, 4, 512, 1500
+    lens = np.array([1500, 1, 700], np.int32)
+    wins = np.array([0, 1024, 100], np.int32)
+    qd, qv = queries(rng, (B, Hq, D), "bf16")
+    k = O.rms_norm(rng.standard_normal((B, Hkv, cap, D)).astype(np.float32))
+    v = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    c = O.quantize_int4(k, "f32") + O.quantize_int4(v, "f32")
+    out = gpu.sdpa_int4_ragged(qd, *[dev(a) for a in c], dev(lens), 8, windows=dev(wins))
+    ref = O.sdpa_int4_ragged(qv, *c, lens, wins, 8)
+    assert_close(host(out), ref, "D512 f32 ragged")
 
 
 @pytest.mark.parametrize("L", [2, 31, 32, 33, 100, 127, 128, 129, 255, 257, 383, 640, 1000])

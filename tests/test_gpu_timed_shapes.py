@@ -59,6 +59,23 @@ def test_headline_launch_32k(gpu, sb):
     assert _lib.last_error() == ""
 
 
+@pytest.mark.parametrize("sb", [torch.float16, torch.float32])
+def test_global_launch_32k(gpu, sb):
+    """bench.py --workload global: Hq 32, Hkv 4 (GQA 8), D 512, L 32768 on
+    the wave-specialised heads-as-columns kernel, for both scale/bias
+    dtypes; two kv heads checked against the C oracle."""
+    from gemma4metal_amd import _lib
+    Hq, Hkv, D, L = 32, 4, 512, 32768
+    assert gpu.sdpa_plan(Hq, Hkv, D, L, sb_dtype=sb)["kernel"] == "sdpa_int4_hc2_kernel"
+    g = torch.Generator(device="cuda").manual_seed(5120)
+    cache = gpu_cache(gpu, Hkv, L, D, g, sb=sb)
+    rng = np.random.default_rng(5120)
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    out = host(gpu.sdpa_int4(qd, *cache, Hq // Hkv, 1.0, 0))
+    check_heads(out, qv, cache, (0, 3), 8, what="global L=32768")
+    assert _lib.last_error() == ""
+
+
 @pytest.mark.parametrize("L", [1024, 131072])
 def test_sweep_points(gpu, L):
     """Sweep lengths of configs[2] not covered elsewhere (8192 and 262144

@@ -18,15 +18,23 @@ def test_headline_plan():
 
 @pytest.mark.parametrize("sb", [F16, F32])
 @pytest.mark.parametrize("Hq,Hkv,D", [(32, 16, 256), (2, 1, 128), (16, 2, 128), (32, 8, 256),
-                                      (8, 4, 512), (8, 8, 512)])
+                                      (8, 4, 512), (8, 8, 512), (12, 4, 512)])
 def test_matrix_core_kernel_for_both_scale_dtypes(Hq, Hkv, D, sb):
     assert tq.sdpa_plan(Hq, Hkv, D, 5000, sb_dtype=sb)["kernel"] == "sdpa_int4_mfma_kernel"
 
 
-def test_global_layer_kernels():
-    # D 512 with GQA 8: heads-as-columns kernel for fp16 scales; fp32 scales
-    # take the matrix-core kernel two heads per workgroup
-    assert tq.sdpa_plan(32, 4, 512, 32768)["kernel"] == "sdpa_int4_hc2_kernel"
+@pytest.mark.parametrize("sb", [F16, F32])
+def test_global_layer_kernels(sb):
+    # D 512 with GQA 8 (Gemma global layers): the wave-specialised
+    # heads-as-columns kernel for both scale/bias dtypes
+    assert tq.sdpa_plan(32, 4, 512, 32768, sb_dtype=sb)["kernel"] == "sdpa_int4_hc2_kernel"
+    assert tq.sdpa_plan(32, 2, 512, 5000, sb_dtype=sb)["kernel"] == "sdpa_int4_hc2_kernel"
+
+
+def test_one_wave_global_kernel_is_fp16_only(tq_env):
+    tq_env("TQ_HC_IMPL", "1")
+    assert tq.sdpa_plan(32, 4, 512, 32768)["kernel"] == "sdpa_int4_hc_kernel"
+    # fp32 scale/bias: the matrix-core kernel, two heads per workgroup
     assert tq.sdpa_plan(32, 4, 512, 32768, sb_dtype=F32)["kernel"] == "sdpa_int4_mfma_kernel"
 
 
