@@ -28,7 +28,8 @@
 //   kept per (column, block) and removed at the end.
 //
 // Lane roles (l = lane, m = l % 16, c = l / 16):
-//   K A-operand: key 16 tile + m, words 8 g + 2c, 8 g + 2c + 1 of group g;
+//   K A-operand of product h of pair P: key 16 tile + m, words
+//   8 (2P + c / 2) + 4 (c % 2) + 2h and + 1 (one 16-byte load per pair);
 //   scores: C rows 4c .. 4c+3 of column m, i.e. keys 16 tile + 4c + i of
 //   head m % 8;  V slot j of lane group c: key 16 (j / 4) + 4c + j % 4 (the
 //   key whose weight this lane computed as C[4c + j % 4] of tile j / 4);
@@ -53,7 +54,7 @@ constexpr int kHcNG = 8;   // quant groups per row
 constexpr int kHcRB = 256; // bytes per packed row
 
 struct HcBuf {
-  uint32_t kw[2][16];  // [tile][4 P + 2 h + e]: word 8 (2P + c/2) + 4h + 2 (c%2) + e of key 16 tile + m
+  uint32_t kw[2][16];  // [tile][4 P + 2 h + e]: word 8 (2P + c/2) + 4 (c%2) + 2h + e of key 16 tile + m
   uint32_t vw[8][4];   // [slot][blk]: word 16 blk + m of the slot's key
   u32x4 sc[2][1];      // scales of array c for keys 2m, 2m+1 (8 fp16 each)
 };
@@ -61,18 +62,21 @@ struct HcBuf {
 // Loads of the 32 keys at t0 (rows clamped to `last`, the uniform limit
 // `lim` = last - t0 >= 0), non-temporal, uniform base + 32-bit lane offset:
 // K words, the scale arrays and the V words, as separate parts.
+// K words: one 16-byte load per (tile, pair P): lane group c takes words
+// 16 P + 4c .. + 3 of its key (group 2P + c / 2, half c % 2 of it), so the 4
+// lane groups of a row read its 64 bytes of the pair contiguously.
 __device__ __forceinline__ void hc_load_kw(uint32_t (&kw)[2][16], const char* kq, int t0, int lim, int m, int c) {
   const char* kb = kq + static_cast<int64_t>(t0) * kHcRB;
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
-    // lane group c takes group 2P + c / 2 of each pair, dims 16 (c % 2) ..
-    // + 15 of each 32-dim half
-    const uint32_t off = static_cast<uint32_t>(min(16 * tile + m, lim)) * kHcRB + 32 * (c >> 1) + 8 * (c & 1);
+    const uint32_t off = static_cast<uint32_t>(min(16 * tile + m, lim)) * kHcRB + 16 * c;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {  // j = 2 P + h
-      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(kb + off + 16 * j + 32 * (j >> 1)));
-      kw[tile][2 * j] = u.x;
-      kw[tile][2 * j + 1] = u.y;
+    for (int P = 0; P < 4; ++P) {
+      const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off + 64 * P));
+      kw[tile][4 * P] = u.x;
+      kw[tile][4 * P + 1] = u.y;
+      kw[tile][4 * P + 2] = u.z;
+      kw[tile][4 * P + 3] = u.w;
     }
   }
 }
@@ -174,12 +178,12 @@ __device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT],
     const int h = k / KPH;
     const int d = (wave * 64 + k * kNT - h * D) + lane;
     X[k] = static_cast<int>(__builtin_rintf(qv[k] * ldexpf(1.0f, sh_F[h])));
-    // k-slot of dim d (group g = d / 64) in the product of pair g / 2 and
-    // half hf = (d % 64) / 32: lane group cc = (d % 32) / 16 + 2 (g % 2),
-    // column h + 8 (g % 2); vector element v = 2 ((d % 16) / 8) + d % 2,
-    // byte (d % 8) / 2 -- the order in which the unpack spreads a word's
-    // nibbles
-    const int g = d >> 6, r = d & 63, hf = r >> 5, cc = ((r >> 4) & 1) + 2 * (g & 1), rr = r & 15;
+    // k-slot of dim d (group g = d / 64, word w = (d % 64) / 8 of the
+    // group) in the products of pair g / 2: lane group cc = w / 4 + 2 (g % 2)
+    // (the lane group that loads the word), product hf = (w / 2) % 2,
+    // column h + 8 (g % 2); vector element v = 2 (w % 2) + d % 2, byte
+    // (d % 8) / 2 -- the order in which the unpack spreads a word's nibbles
+    const int g = d >> 6, r = d & 63, hf = (r >> 4) & 1, cc = (r >> 5) + 2 * (g & 1), rr = r & 15;
     const int s = 4 * (2 * (rr >> 3) + (rr & 1)) + ((rr & 7) >> 1);
     const int d0 = static_cast<int8_t>(X[k] & 0xFF);
     const int X1 = (X[k] - d0) >> 8;
