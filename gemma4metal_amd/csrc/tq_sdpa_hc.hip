@@ -65,20 +65,23 @@ struct HcBuf {
 // K words: one 16-byte load per (tile, pair P): lane group c takes words
 // 16 P + 4c .. + 3 of its key (group 2P + c / 2, half c % 2 of it), so the 4
 // lane groups of a row read its 64 bytes of the pair contiguously.
-__device__ __forceinline__ void hc_load_kw(uint32_t (&kw)[2][16], const char* kq, int t0, int lim, int m, int c) {
+__device__ __forceinline__ void hc_load_kw_pair(uint32_t (&kw)[2][16], const char* kq, int t0, int lim, int m,
+                                                int c, int P) {
   const char* kb = kq + static_cast<int64_t>(t0) * kHcRB;
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
     const uint32_t off = static_cast<uint32_t>(min(16 * tile + m, lim)) * kHcRB + 16 * c;
-#pragma unroll
-    for (int P = 0; P < 4; ++P) {
-      const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off + 64 * P));
-      kw[tile][4 * P] = u.x;
-      kw[tile][4 * P + 1] = u.y;
-      kw[tile][4 * P + 2] = u.z;
-      kw[tile][4 * P + 3] = u.w;
-    }
+    const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kb + off + 64 * P));
+    kw[tile][4 * P] = u.x;
+    kw[tile][4 * P + 1] = u.y;
+    kw[tile][4 * P + 2] = u.z;
+    kw[tile][4 * P + 3] = u.w;
   }
+}
+
+__device__ __forceinline__ void hc_load_kw(uint32_t (&kw)[2][16], const char* kq, int t0, int lim, int m, int c) {
+#pragma unroll
+  for (int P = 0; P < 4; ++P) hc_load_kw_pair(kw, kq, t0, lim, m, c, P);
 }
 
 // Scale array of lane group c (k scale, k bias, v scale, v bias) for keys
@@ -115,6 +118,52 @@ __device__ __forceinline__ void hc_load_v(uint32_t (&vw)[8][4], const char* vq, 
   }
 }
 
+// V words for the wave-specialised kernel: one 16-byte load per (tile T,
+// block blk): lane (m = 4 qd + i, c) loads words 16 blk + 4 qd .. + 3 of key
+// 16 T + 4c + i, so a quad of lanes reads 4 keys x 16 contiguous bytes.
+// hc_quad_transpose then gives lane i of the quad word 16 blk + 4 qd + i of
+// keys 16 T + 4c + 0 .. 3: the slots 4T .. 4T + 3 of hc_load_v's layout.
+__device__ __forceinline__ void hc_load_v4_blk(u32x4 (&vr)[2][4], const char* vq, int t0, int lim, int m, int c,
+                                               int blk) {
+  const char* vb = vq + static_cast<int64_t>(t0) * kHcRB;
+#pragma unroll
+  for (int T = 0; T < 2; ++T) {
+    const uint32_t off = static_cast<uint32_t>(min(16 * T + 4 * c + (m & 3), lim)) * kHcRB + 16 * (m >> 2);
+    vr[T][blk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vb + off + 64 * blk));
+  }
+}
+
+__device__ __forceinline__ void hc_load_v4(u32x4 (&vr)[2][4], const char* vq, int t0, int lim, int m, int c) {
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) hc_load_v4_blk(vr, vq, t0, lim, m, c, blk);
+}
+
+// 4 x 4 transpose of dwords inside each quad of lanes: lane i of the quad
+// returns R[i] of lanes 0 .. 3.  Two butterfly stages on DPP quad_perm
+// (lane ^ 2, then lane ^ 1), each exchanging one bit of the register index
+// with the same bit of the lane index.
+__device__ __forceinline__ u32x4 hc_quad_transpose(u32x4 R, int lane) {
+  const bool i1 = (lane & 2) != 0, i0 = (lane & 1) != 0;
+  uint32_t U[4], W[4];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const uint32_t X = i1 ? R[x] : R[2 + x];
+    const uint32_t Y = static_cast<uint32_t>(
+        __builtin_amdgcn_mov_dpp(static_cast<int>(X), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    U[x] = i1 ? Y : R[x];
+    U[2 + x] = i1 ? R[2 + x] : Y;
+  }
+#pragma unroll
+  for (int y = 0; y < 4; y += 2) {
+    const uint32_t X = i0 ? U[y] : U[y + 1];
+    const uint32_t Y = static_cast<uint32_t>(
+        __builtin_amdgcn_mov_dpp(static_cast<int>(X), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    W[y] = i0 ? Y : U[y];
+    W[y + 1] = i0 ? U[y + 1] : Y;
+  }
+  return u32x4{W[0], W[1], W[2], W[3]};
+}
+
 __device__ __forceinline__ void hc_load(HcBuf& B, const char* kq, const char* vq, const char* sc,
                                         int t0, int lim, int m, int c) {
   hc_load_k(B.kw, B.sc, kq, sc, t0, lim, m, c);
@@ -125,85 +174,132 @@ __device__ __forceinline__ float hc_half(uint32_t w, int hi) {
   return __half2float(__ushort_as_half(static_cast<uint16_t>(hi ? (w >> 16) : (w & 0xFFFFu))));
 }
 
-// Prologue of both kernels: the scaled q of the 8 heads (qv[k] = element
-// threadIdx.x + kNT k of the 8 x 512 block) as 21-bit fixed point, scattered
-// into the block-diagonal B images of the K.q products (bq_lds, whose
-// off-diagonal blocks are zeroed here), the per-(head, group) sums of the
-// fixed-point q (sh_qhat) and the per-head exponent F (sh_F).  NW = waves of
-// the workgroup.  Ends with a barrier.
-template <int kNT, int NW>
-__device__ __forceinline__ void hc_q_image(const float (&qv)[kHcG * kHcD / kNT], uint4 (&bq_lds)[3][kHcNG][64],
-                                           float (&red_max)[kHcG * kHcD / kNT][NW],
-                                           float (&sh_qhat)[kHcG][kHcNG], int (&sh_F)[kHcG], int lane,
-                                           int wave) {
-  constexpr int D = kHcD, G = kHcG, NG = kHcNG, NE = G * D / kNT;
-  static_assert(D % kNT == 0, "slot -> head");
-  // slot (k, w) = elements 64 w + kNT k + lane: one quant group of head
-  // (kNT k) / D (kNT divides D, so k alone names the head)
-  constexpr int KPH = D / kNT;  // slots k per head
-  {
-    float mx[NE];
+// Prologue of both kernels: the workgroup's q (8 heads x 512, one contiguous
+// block) as 21-bit fixed point per head, scattered into the block-diagonal B
+// images of the K.q products (bq_lds, whose off-diagonal blocks are zeroed
+// here), with the per-(head, group) sums of the fixed-point q (sh_qhat) and
+// the per-head exponent F (sh_F).  Thread t takes the 8-element chunks
+// t + kNT i: a wave's 64 chunks are the 512 dims of one head, so the head's
+// maximum is a wave reduction, and a chunk is one word (8 dims) of one quant
+// group, whose three base-256 digits fill two whole dwords of one lane's B
+// operand each.
+template <int kNT>
+struct HcQ {
+  static constexpr int NCH = kHcG * kHcD / 8 / kNT;  // chunks per thread
+  u32x4 raw[NCH][2];                                 // 8 elements (fp32: both vectors)
+};
+
+template <int kNT>
+__device__ __forceinline__ void hc_q_load(HcQ<kNT>& Q, const SdpaParams& p, int64_t qbase) {
+  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+  const char* qb = static_cast<const char*>(p.q) + qbase * qsz;
+  const bool al16 = (reinterpret_cast<uintptr_t>(qb) & 15) == 0;  // uniform
 #pragma unroll
-    for (int k = 0; k < NE; ++k) mx[k] = wave_max_dpp(fabsf(qv[k]));
-    if (lane == 0) {
+  for (int i = 0; i < HcQ<kNT>::NCH; ++i) {
+    const char* src = qb + static_cast<int64_t>(threadIdx.x + kNT * i) * 8 * qsz;
+    if (al16) {
+      Q.raw[i][0] = *reinterpret_cast<const u32x4*>(src);
+      Q.raw[i][1] = qsz == 4 ? *reinterpret_cast<const u32x4*>(src + 16) : Q.raw[i][0];
+    } else if (qsz == 4) {
+      const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
+      Q.raw[i][0] = u32x4{s32[0], s32[1], s32[2], s32[3]};
+      Q.raw[i][1] = u32x4{s32[4], s32[5], s32[6], s32[7]};
+    } else {
+      const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src);
+      uint32_t w[4];
 #pragma unroll
-      for (int k = 0; k < NE; ++k) red_max[k][wave] = mx[k];
+      for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(s16[2 * j]) | (static_cast<uint32_t>(s16[2 * j + 1]) << 16);
+      Q.raw[i][0] = u32x4{w[0], w[1], w[2], w[3]};
+      Q.raw[i][1] = Q.raw[i][0];
     }
   }
+}
+
+// Exact int32 sum over aligned groups of 8 lanes (DPP butterfly in the row).
+__device__ __forceinline__ int group8_sum_i(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // lane ^ 1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // lane ^ 2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // half-row mirror
+  return v;
+}
+
+// Ends with a barrier.
+template <int kNT>
+__device__ __forceinline__ void hc_q_build(const HcQ<kNT>& Q, const SdpaParams& p, uint4 (&bq_lds)[3][kHcNG][64],
+                                           float (&sh_qhat)[kHcG][kHcNG], int (&sh_F)[kHcG], int lane) {
+  constexpr int NG = kHcNG;
   {
-    // the off-diagonal blocks of the B images stay zero
+    // the off-diagonal blocks of the B images stay zero: lane 16c + n of an
+    // image is nonzero only where column n takes the group of lane group c
+    // ((n >= 8) == (c >= 2)); the two sets are disjoint, so no barrier
+    // separates these stores from the digit stores below
     uint4* z = &bq_lds[0][0][0];
-    for (int i = threadIdx.x; i < 3 * NG * 64; i += kNT) z[i] = uint4{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < 3 * NG * 32; i += kNT) {
+      const int cz = (i >> 3) & 3, nz = (i & 7) + ((cz >> 1) ? 0 : 8);
+      z[(i >> 5) * 64 + 16 * cz + nz] = uint4{0u, 0u, 0u, 0u};
+    }
   }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int h = threadIdx.x;
-    float hm = 0.0f;
+  uint8_t* bq_bytes = reinterpret_cast<uint8_t*>(&bq_lds[0][0][0]);
+  // this lane's chunk: word w of quant group g; in the products of pair
+  // g / 2 it is loaded by lane group cc = w / 4 + 2 (g % 2) as product
+  // hf = (w / 2) % 2, vector elements 2 (w % 2) (even dims) and + 1 (odd
+  // dims), byte (d % 8) / 2 -- the order in which the unpack spreads a
+  // word's nibbles
+  const int g = lane >> 3, w = lane & 7;
+  const int cc = (w >> 2) + 2 * (g & 1), hf = (w >> 1) & 1, e = w & 1;
 #pragma unroll
-    for (int k2 = 0; k2 < KPH; ++k2)
+  for (int i = 0; i < HcQ<kNT>::NCH; ++i) {
+    const int head = static_cast<int>((threadIdx.x + kNT * i) >> 6);
+    float qv[8];
+    float mx = 0.0f;
 #pragma unroll
-      for (int w2 = 0; w2 < NW; ++w2) hm = fmaxf(hm, red_max[h * KPH + k2][w2]);
+    for (int t = 0; t < 8; ++t) {
+      float f;
+      if (p.q_dtype == TQ_F32) {
+        f = __uint_as_float(Q.raw[i][t >> 2][t & 3]);
+      } else {
+        const uint32_t wd = Q.raw[i][0][t >> 1];
+        const uint32_t h16 = (t & 1) ? (wd >> 16) : (wd & 0xFFFFu);
+        f = p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(h16)))
+                                : __uint_as_float(h16 << 16);
+      }
+      qv[t] = f * p.scale_log2;
+      mx = fmaxf(mx, fabsf(qv[t]));
+    }
+    mx = wave_max_dpp(mx);
     int ex = 0;
-    if (hm > 0.0f) frexpf(hm, &ex);  // hm < 2^ex
+    if (mx > 0.0f) frexpf(mx, &ex);  // mx < 2^ex
     // |round(q * 2^F)| <= 2^21: the top base-256 digit is then within
     // [-32, 32], and a group's dot sum_d nibble_d * X_d (|.| <= 64 * 15 *
     // 2^21 < 2^31) is exact in int32
-    sh_F[h] = 21 - ex;
-  }
-  __syncthreads();
-  uint8_t* bq_bytes = reinterpret_cast<uint8_t*>(&bq_lds[0][0][0]);
-  int X[NE];
+    const int F = 21 - ex;
+    const float up = ldexpf(1.0f, F);
+    uint32_t ev[3] = {0u, 0u, 0u}, od[3] = {0u, 0u, 0u};
+    int xs = 0;
 #pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const int h = k / KPH;
-    const int d = (wave * 64 + k * kNT - h * D) + lane;
-    X[k] = static_cast<int>(__builtin_rintf(qv[k] * ldexpf(1.0f, sh_F[h])));
-    // k-slot of dim d (group g = d / 64, word w = (d % 64) / 8 of the
-    // group) in the products of pair g / 2: lane group cc = w / 4 + 2 (g % 2)
-    // (the lane group that loads the word), product hf = (w / 2) % 2,
-    // column h + 8 (g % 2); vector element v = 2 (w % 2) + d % 2, byte
-    // (d % 8) / 2 -- the order in which the unpack spreads a word's nibbles
-    const int g = d >> 6, r = d & 63, hf = (r >> 4) & 1, cc = (r >> 5) + 2 * (g & 1), rr = r & 15;
-    const int s = 4 * (2 * (rr >> 3) + (rr & 1)) + ((rr & 7) >> 1);
-    const int d0 = static_cast<int8_t>(X[k] & 0xFF);
-    const int X1 = (X[k] - d0) >> 8;
-    const int d1 = static_cast<int8_t>(X1 & 0xFF);
-    const int d2 = (X1 - d1) >> 8;
-    const int ln = 16 * cc + h + 8 * (g & 1);
-    const int o = (((g >> 1) * 2 + hf) * 64 + ln) * 16 + s;
-    bq_bytes[o] = static_cast<uint8_t>(d0);
-    bq_bytes[o + NG * 64 * 16] = static_cast<uint8_t>(d1);
-    bq_bytes[o + 2 * NG * 64 * 16] = static_cast<uint8_t>(d2);
-  }
-  // per (head, quant group) sums of the fixed-point q, exact: 64 * 2^21 < 2^31
-#pragma unroll
-  for (int k = 0; k < NE; ++k) X[k] = wave_sum_dpp(X[k]);
-  if (lane == 0) {
-#pragma unroll
-    for (int k = 0; k < NE; ++k) {
-      const int h = k / KPH, g = (wave * 64 + k * kNT - h * D) >> 6;
-      sh_qhat[h][g] = static_cast<float>(X[k]) * ldexpf(1.0f, -sh_F[h]);
+    for (int t = 0; t < 8; ++t) {
+      const int X = static_cast<int>(__builtin_rintf(qv[t] * up));
+      xs += X;
+      const int d0 = static_cast<int8_t>(X & 0xFF);
+      const int X1 = (X - d0) >> 8;
+      const int d1 = static_cast<int8_t>(X1 & 0xFF);
+      const int d2 = (X1 - d1) >> 8;
+      const int sh = 8 * (t >> 1);
+      uint32_t* dst = (t & 1) ? od : ev;
+      dst[0] |= static_cast<uint32_t>(d0 & 0xFF) << sh;
+      dst[1] |= static_cast<uint32_t>(d1 & 0xFF) << sh;
+      dst[2] |= static_cast<uint32_t>(d2 & 0xFF) << sh;
     }
+    const int ln = 16 * cc + head + 8 * (g & 1);
+    const int o = (((g >> 1) * 2 + hf) * 64 + ln) * 16 + 8 * e;
+#pragma unroll
+    for (int dg = 0; dg < 3; ++dg)
+      *reinterpret_cast<u32x2*>(bq_bytes + o + dg * NG * 64 * 16) = u32x2{ev[dg], od[dg]};
+    // per (head, quant group) sum of the fixed-point q over the group's 8
+    // lanes, exact: 64 * 2^21 < 2^31
+    xs = group8_sum_i(xs);
+    if (w == 0) sh_qhat[head][g] = static_cast<float>(xs) * ldexpf(1.0f, -F);
+    if (lane == 0) sh_F[head] = F;
   }
   __syncthreads();
 }
@@ -214,7 +310,6 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   constexpr int NW = kHcWaves, D = kHcD, G = kHcG, NG = kHcNG;
   constexpr int kNT = NW * 64;
   constexpr int kIter = 32 * NW;          // keys per workgroup iteration
-  constexpr int NE = G * D / kNT;         // q elements per thread
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;
@@ -231,7 +326,6 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   __shared__ __attribute__((aligned(16))) float arena[Fin::kArena];
   __shared__ uint4 bq_lds[3][NG][64];           // K MFMA B operands [digit][2 pair + half][lane]
   __shared__ uint32_t sc_lds[NW][4][NG][16];    // [wave][array][group][key pair] fp16 x 2
-  __shared__ float red_max[NE][NW];
   __shared__ float sh_qhat[G][NG];
   __shared__ int sh_F[G];
 
@@ -248,20 +342,10 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   const int last = t_end - 1;
   const int safe_last = max(last, 0);
 
-  // q first (one dword per element, no branch around the load), then the
-  // first iteration's K/V, which stay in flight through the prologue.  A
-  // 16-bit element's half of its dword depends on the element's index only
-  // (kNT is even), and is selected at conversion: shifting right after the
-  // load would wait for q before the K/V loads go out.
-  uint32_t qraw[NE];
-  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
-  const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
-  const uint32_t qsh = qsz == 2 && ((qbase + threadIdx.x) & 1) ? 16u : 0u;
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
-    qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-  }
+  // q first, then the first iteration's K/V, which stay in flight through
+  // the prologue
+  HcQ<kNT> Q;
+  hc_q_load<kNT>(Q, p, (static_cast<int64_t>(b) * p.Hq + h0) * D);
   __builtin_amdgcn_sched_barrier(0);
   HcBuf bufA, bufB;
   {
@@ -271,16 +355,7 @@ void sdpa_int4_hc_kernel(SdpaParams p) {
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue: q of the 8 heads as 21-bit fixed point, B images in LDS --
-  float qv[NE];
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const uint32_t w = qraw[k] >> qsh;
-    const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
-                    : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
-                                          : __uint_as_float(w << 16);
-    qv[k] = f * p.scale_log2;
-  }
-  hc_q_image<kNT, NW>(qv, bq_lds, red_max, sh_qhat, sh_F, lane, wave);
+  hc_q_build<kNT>(Q, p, bq_lds, sh_qhat, sh_F, lane);
   const float sf = ldexpf(1.0f, -sh_F[hh]);
   // q sums of this lane's column: head hh, group 2P + m / 8 of pair P
   float qh[NG / 2];
@@ -518,7 +593,6 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   constexpr int NS = kHs, NWV = 2 * kHs, D = kHcD, G = kHcG, NG = kHcNG;
   constexpr int kNT = NWV * 64;
   constexpr int kIter = 32 * NS;   // keys per workgroup iteration
-  constexpr int NE = G * D / kNT;  // q elements per thread
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;
@@ -543,7 +617,6 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t sc_lds[NS][4][NG][SK];
   __shared__ float f_lds[2][NS][16];          // rescale factor per column, by slot
   __shared__ float off_lds[NS][4][16];        // final offset per (block, column)
-  __shared__ float red_max[NE][NWV];
   __shared__ float sh_qhat[G][NG];
   __shared__ int sh_F[G];
 
@@ -565,37 +638,13 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   const int safe_last = max(last, 0);
   auto tclamp = [&](int t0) { return min(t0, safe_last); };
 
-  // q: one dword per element; a 16-bit element's half of its dword depends
-  // on the element's index only (kNT is even) and is selected at conversion,
-  // so the K/V loads issued after q do not wait for it
-  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
   const int64_t qbase = (static_cast<int64_t>(b) * p.Hq + h0) * D;
-  const uint32_t qsh = qsz == 2 && ((qbase + threadIdx.x) & 1) ? 16u : 0u;
-  auto load_q = [&](uint32_t (&qraw)[NE]) {
-#pragma unroll
-    for (int k = 0; k < NE; ++k) {
-      const int64_t byte = (qbase + threadIdx.x + k * kNT) * qsz;
-      qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-    }
-  };
-  auto q_image = [&](const uint32_t (&qraw)[NE]) {
-    float qv[NE];
-#pragma unroll
-    for (int k = 0; k < NE; ++k) {
-      const uint32_t w = qraw[k] >> qsh;
-      const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
-                      : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
-                                            : __uint_as_float(w << 16);
-      qv[k] = f * p.scale_log2;
-    }
-    hc_q_image<kNT, NWV>(qv, bq_lds, red_max, sh_qhat, sh_F, lane, wave);
-  };
   const v4i zero4 = v4i{0, 0, 0, 0};
 
   if (producer) {
     // ======================= producer: K . q, softmax, B operands ===========
-    uint32_t qraw[NE];
-    load_q(qraw);
+    HcQ<kNT> Q;
+    hc_q_load<kNT>(Q, p, qbase);
     __builtin_amdgcn_sched_barrier(0);
     constexpr int SW = F32 ? 2 : 1;  // 16-byte scale vectors per key
     uint32_t kA[2][16], kB[2][16];
@@ -607,7 +656,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     };
     load_k(kA, sA, base0);
     __builtin_amdgcn_sched_barrier(0);
-    q_image(qraw);
+    hc_q_build<kNT>(Q, p, bq_lds, sh_qhat, sh_F, lane);
     const float sf = ldexpf(1.0f, -sh_F[hh]);
     float qh[NG / 2];
 #pragma unroll
@@ -618,8 +667,13 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) wsum[blk] = bacc[blk] = 0.0f;
 
-    auto produce = [&](const uint32_t (&kw)[2][16], const u32x4 (&scw)[2][SW], int st) {
+    // One step: this step's products, with the next step's K and scale
+    // loads issued among them (scales first, then two K loads per pair), so
+    // the wave never stalls on a burst of loads after the barrier.
+    auto produce = [&](const uint32_t (&kw)[2][16], const u32x4 (&scw)[2][SW], int st, uint32_t (&nk)[2][16],
+                       u32x4 (&ns)[2][SW]) {
       const int t0 = base0 + st * kIter, slot = st & 1;
+      const int tn = tclamp(t0 + kIter);
       // scales -> LDS [array][group][key pair] (fp16) or [..][key] (fp32)
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
@@ -643,6 +697,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      __builtin_amdgcn_sched_barrier(0);
+      hc_load_sc<F32>(ns, sc_rows, tn, safe_last - tn, m);
+      __builtin_amdgcn_sched_barrier(0);
 
       // K . q per pair of quant groups (as in the kernel above)
       float sc[2][4];
@@ -681,6 +738,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
             sc[tile][i] = fmaf(dot, ks[i], fmaf(kb[i], qh[P], sc[tile][i]));
           }
         }
+        __builtin_amdgcn_sched_barrier(0);
+        hc_load_kw_pair(nk, kq_rows, tn, safe_last - tn, m, c, P);
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile)
@@ -745,13 +805,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     };
 
     for (int st = 0; st < NI; st += 2) {
-      load_k(kB, sB, base0 + (st + 1) * kIter);
-      __builtin_amdgcn_sched_barrier(0);
-      produce(kA, sA, st);
+      produce(kA, sA, st, kB, sB);
       __syncthreads();
-      load_k(kA, sA, base0 + (st + 2) * kIter);
-      __builtin_amdgcn_sched_barrier(0);
-      produce(kB, sB, st + 1);
+      produce(kB, sB, st + 1, kA, sA);
       __syncthreads();
     }
     __syncthreads();  // the consumers' last step
@@ -775,13 +831,13 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     __syncthreads();  // offsets visible to the consumers
   } else {
     // ======================= consumer: P . V ================================
-    uint32_t qraw[NE];
-    load_q(qraw);
-    __builtin_amdgcn_sched_barrier(0);
-    uint32_t vA[8][4], vB[8][4];
-    hc_load_v(vA, vq_rows, tclamp(base0), safe_last - tclamp(base0), m, c);
-    __builtin_amdgcn_sched_barrier(0);
-    q_image(qraw);
+    // the first V loads go out after the q image: this wave's first products
+    // wait for the producers' first step anyway
+    HcQ<kNT> Q;
+    hc_q_load<kNT>(Q, p, qbase);
+    hc_q_build<kNT>(Q, p, bq_lds, sh_qhat, sh_F, lane);
+    u32x4 vA[2][4], vB[2][4];
+    hc_load_v4(vA, vq_rows, tclamp(base0), safe_last - tclamp(base0), m, c);
 
     v4f cv[4][8];  // [blk][2 byte + nibble half]
 #pragma unroll
@@ -791,7 +847,10 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     uint32_t magic = 0x43004300u;  // bf16 of (128 + nibble)
     asm volatile("" : "+v"(magic));
 
-    auto consume = [&](const uint32_t (&vw)[8][4], int st) {
+    // One step: this step's products, with the next step's V loads issued
+    // among them (two per block).
+    auto consume = [&](const u32x4 (&vr)[2][4], int st, u32x4 (&nx)[2][4]) {
+      const int tn = tclamp(base0 + (st + 1) * kIter);
       const int slot = st & 1;
       const float f = f_lds[slot][s][m];
       if (__any(f != 1.0f)) {
@@ -802,6 +861,17 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       }
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
+        // slot j = 4T + i: word 16 blk + m of key 16 T + 4c + i
+        uint32_t vw[8];
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+          const u32x4 t = hc_quad_transpose(vr[T][blk], lane);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vw[4 * T + i] = t[i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        hc_load_v4_blk(nx, vq_rows, tn, safe_last - tn, m, c, blk);
+        __builtin_amdgcn_sched_barrier(0);
         const uint4* src = pv_lds + (((slot * NS + s) * 4 + blk) * 2) * 64 + lane;
         const v8bf bhi = __builtin_bit_cast(v8bf, src[0]);
         const v8bf blo = __builtin_bit_cast(v8bf, src[64]);
@@ -812,7 +882,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
           uint32_t alo[4], ahi[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const uint32_t x = __builtin_amdgcn_perm(vw[2 * r + 1][blk], vw[2 * r][blk], sel);
+            const uint32_t x = __builtin_amdgcn_perm(vw[2 * r + 1], vw[2 * r], sel);
             alo[r] = (x & 0x000F000Fu) | magic;
             ahi[r] = ((x >> 4) & 0x000F000Fu) | magic;
           }
@@ -828,13 +898,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 
     __syncthreads();  // the producers' step 0
     for (int st = 0; st < NI; st += 2) {
-      hc_load_v(vB, vq_rows, tclamp(base0 + (st + 1) * kIter), safe_last - tclamp(base0 + (st + 1) * kIter), m, c);
-      __builtin_amdgcn_sched_barrier(0);
-      consume(vA, st);
+      consume(vA, st, vB);
       __syncthreads();
-      hc_load_v(vA, vq_rows, tclamp(base0 + (st + 2) * kIter), safe_last - tclamp(base0 + (st + 2) * kIter), m, c);
-      __builtin_amdgcn_sched_barrier(0);
-      consume(vB, st + 1);
+      consume(vB, st + 1, vA);
       __syncthreads();
     }
     __syncthreads();  // the producers' offsets
