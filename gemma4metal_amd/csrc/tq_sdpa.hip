@@ -514,6 +514,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
       set_error("%s: workspace of %zu bytes needed (got %zu)", fn, wl.total, ws_bytes);
       return TQ_ERR_WORKSPACE;
     }
+    TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "%s: workspace must be 16-byte aligned", fn);
   }
   TQ_CHECK_ARG(Hkv * n_sub <= 65535 && batch <= 65535, "%s: grid too large", fn);
   TQ_CHECK_ARG(static_cast<int64_t>(batch) * Hq <= kMaxCounters || (prefill && max_splits == 1),

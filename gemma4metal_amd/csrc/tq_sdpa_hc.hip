@@ -605,11 +605,15 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
   if (split >= rg.S) return;
   const int t_end = rg.t_end;
 
-  using Fin = Finalize<G, D, NS, kNT>;
-  // the P . V operand slots during the loop, the finalisation arena after it
+  // the P . V operand slots during the loop; after it, the streams' partial
+  // outputs [stream][head][D + 4] (rows padded by 16 bytes, so the 8 heads'
+  // rows start in different LDS banks)
   constexpr int kPvWords = 2 * NS * 4 * 2 * 64 * 4;  // [slot][stream][blk][hi/lo][lane] x uint4
-  constexpr int kArenaWords = Fin::kArena > kPvWords ? Fin::kArena : kPvWords;
+  constexpr int kRow = D + 4;
+  constexpr int kOWords = NS * G * kRow;
+  constexpr int kArenaWords = kOWords > kPvWords ? kOWords : kPvWords;
   __shared__ __attribute__((aligned(16))) float arena[kArenaWords];
+  __shared__ float ml_lds[2][NS][G];          // per stream: running max, sum of weights
   uint4* pv_lds = reinterpret_cast<uint4*>(arena);
   __shared__ uint4 bq_lds[3][NG][64];         // K MFMA B operands [digit][2 pair + half][lane]
   // [stream][array][group][key pair] fp16 x 2, or [..][key] fp32
@@ -810,10 +814,8 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       produce(kB, sB, st + 1, kA, sA);
       __syncthreads();
     }
-    __syncthreads();  // the consumers' last step
-
-    // per-column results: (m, l) into the arena (the operand slots are dead
-    // now), the offsets of the weight sums for the consumers
+    // per-column results, published by the barrier that ends the consumers'
+    // last step: (m, l) and the offsets of the weight sums
     float l_sum = xor16_sum(l_run);
     l_sum = xor32_sum(l_sum);
 #pragma unroll
@@ -825,10 +827,10 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       if (c == 0) off_lds[s][blk][m] = bacc[blk] - 128.0f * wsum[blk];
     }
     if (c == 0 && m < 8) {
-      Fin::m(arena, s)[hh] = m_run;
-      Fin::l(arena, s)[hh] = l_sum;
+      ml_lds[0][s][hh] = m_run;
+      ml_lds[1][s][hh] = l_sum;
     }
-    __syncthreads();  // offsets visible to the consumers
+    __syncthreads();  // the consumers' last step
   } else {
     // ======================= consumer: P . V ================================
     // the first V loads go out after the q image: this wave's first products
@@ -903,11 +905,12 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       consume(vB, st + 1, vA);
       __syncthreads();
     }
-    __syncthreads();  // the producers' offsets
+    // the operand slots are dead (every consumer passed its last step) and
+    // the producers' offsets visible: the stream's partial into its rows.
     // lane (m, c) holds V words 16 blk + 4c + i of column m; the column's
     // group in block blk is 2 blk + m / 8, the words' group 2 blk + c / 2
     if ((c >> 1) == (m >> 3)) {
-      float* o = Fin::o(arena, s, hh);
+      float* o = arena + (s * G + hh) * kRow;
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
         const float off = off_lds[s][blk][m];
@@ -921,7 +924,41 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
       }
     }
   }
-  Fin::run(p, arena, static_cast<int64_t>(b) * p.Hq + h0, rg.S, split, b * p.Hq + hy);
+  __syncthreads();
+
+  // ---- the four streams combined, four dims per thread ---------------------
+  // The split's partial (or, for a single split, the output) of the 8 heads;
+  // the partials are merged by merge_splits_kernel after this kernel.
+  constexpr int D4 = D / 4;
+  for (int i = threadIdx.x; i < G * D4; i += kNT) {
+    const int h = i / D4, d4 = i - h * D4;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NS; ++w) M = fmaxf(M, ml_lds[0][w][h]);
+    v4f O = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NS; ++w) {
+      const float f = merge_factor(ml_lds[0][w][h], M);
+      O += f * *reinterpret_cast<const v4f*>(arena + (w * G + h) * kRow + 4 * d4);
+      L = fmaf(ml_lds[1][w][h], f, L);
+    }
+    const int64_t row = static_cast<int64_t>(b) * p.Hq + h0 + h;
+    if (rg.S == 1) {
+      const v4f r = v4f{normalise(O[0], L, p.denom_eps), normalise(O[1], L, p.denom_eps),
+                        normalise(O[2], L, p.denom_eps), normalise(O[3], L, p.denom_eps)};
+      float* dst = p.out + row * D + 4 * d4;
+      if ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) {  // uniform
+        *reinterpret_cast<v4f*>(dst) = r;
+      } else {
+        dst[0] = r[0]; dst[1] = r[1]; dst[2] = r[2]; dst[3] = r[3];
+      }
+    } else {
+      const int64_t slot = row * p.max_splits + split;
+      *reinterpret_cast<v4f*>(p.ws_o + slot * D + 4 * d4) = O;
+      if (d4 == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
+    }
+  }
 }
 
 // Merge of split partials written with ext_merge = 1.  A wave takes four

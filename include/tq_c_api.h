@@ -79,8 +79,8 @@ int tq_stream_read_tiles(const void* src, size_t bytes, uint32_t* sink, int bloc
  *   head_dim in {128, 256, 512}; num_heads == num_kv_heads * gqa_factor
  *   kv_capacity >= kv_len is the row stride of each head (== kv_len for a
  *   tight [Hkv, N, .] tensor as in the reference).
- * workspace: >= tq_sdpa_int4_workspace_size(...) bytes, zero-filled once
- * before first use.  Its first 256 KiB hold split counters that every call
+ * workspace: >= tq_sdpa_int4_workspace_size(...) bytes, 16-byte aligned,
+ * zero-filled once before first use.  Its first 256 KiB hold split counters that every call
  * returns to zero, so one workspace may serve calls of any shape one after
  * another on a stream; calls that run concurrently need separate workspaces.
  * batch * num_heads must not exceed 65536. */

@@ -62,6 +62,7 @@ def sdpa(**over):
     (dict(kq=ctypes.c_void_p(0x10004)), 1, "aligned"),
     (dict(scale=float("inf")), 1, "scale"),
     (dict(n=4096, cap=4096), 4, "workspace"),
+    (dict(n=4096, cap=4096, ws=ctypes.c_void_p(0x10008), wsb=1 << 30), 1, "workspace must be 16-byte"),
 ])
 def test_sdpa_rejects_bad_arguments_on_host(over, status, needle):
     st, msg = sdpa(**over)
