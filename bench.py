@@ -258,9 +258,11 @@ def main():
         for label, Hq_, Hkv_, D_, W in (("sliding layer", 32, 16, 256, 1024),
                                          ("global layer", 32, 4, 512, 0)):
             L = prior + S
-            cache = gen_cache(tq, torch, Hkv_, L, D_, gen)
+            cache = gen_cache(tq, torch, Hkv_, L, D_, gen, sb=sbt)
             q = gen_q(torch, (S, Hq_, D_), gen)
             out = torch.empty((S, Hq_, D_), dtype=torch.float32, device="cuda")
+            plan = tq.sdpa_plan(Hq_, Hkv_, D_, L, mode="prefill", batch=S, sliding_window=W,
+                                sb_dtype=sbt)
             ms, _, _ = time_launches(torch, lambda i: tq.sdpa_int4_prefill(
                 q, *cache, prior, Hq_ // Hkv_, 1.0, W, out=out), args.steps, args.warmup)
             keys = sum(min(prior + i + 1, W) if W else prior + i + 1 for i in range(S))
@@ -269,10 +271,13 @@ def main():
                   "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
                   "warmup": args.warmup, "ms_per_step": round(ms, 5),
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-                  "dtype": "int4 K/V (fp16 scale/bias), bf16 Q", "data": "synthetic",
+                  "dtype": (f"int4 K/V ({args.sb} scale/bias), bf16 Q; K dequantized to fp16 hi+lo "
+                            "(q.k as three fp16 matrix-core products, ~22-bit), V and P as bf16 "
+                            "hi+lo, fp32 accumulate"),
+                  "data": "synthetic", "kernel": plan["kernel"],
                   "config": {"workload": f"prefill n_new={S} n_prior={prior} Hq={Hq_} Hkv={Hkv_} "
-                                         f"D={D_} W={W}", "global_batch": 1, "seq_len": L,
-                             "parallelism": "none (1 GPU)"}}, args)
+                                         f"D={D_} W={W}, {args.sb} scale/bias", "global_batch": 1,
+                             "seq_len": L, "parallelism": "none (1 GPU)"}}, args)
         return
 
     if args.workload == "global":

@@ -23,6 +23,8 @@
 // column m; each row has its own causal / window limit.
 #include "tq_sdpa_common.h"
 
+#include <type_traits>
+
 namespace tq {
 namespace {
 
@@ -49,14 +51,18 @@ struct PfGeom {
   static_assert(KPT == 2 || KPT == 4 || KPT == 8, "D");
 };
 
-// Raw int4 words and fp16 scale / bias of this thread's keys of one tile.
-template <int D>
+// Raw int4 words and the scale / bias (fp16 bits, or fp32 with F32) of
+// this thread's keys of one tile.
+template <int D, bool F32>
 struct PfRaw {
+  using SB = typename std::conditional<F32, float, uint16_t>::type;
   uint32_t kw[PfGeom<D>::KPT], vw[PfGeom<D>::KPT];
-  uint16_t ks[PfGeom<D>::KPT], kb[PfGeom<D>::KPT], vs[PfGeom<D>::KPT], vb[PfGeom<D>::KPT];
+  SB ks[PfGeom<D>::KPT], kb[PfGeom<D>::KPT], vs[PfGeom<D>::KPT], vb[PfGeom<D>::KPT];
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ float sbf(uint16_t h) { return h2f(h); }
+__device__ __forceinline__ float sbf(float x) { return x; }
 
 // K and V use different thread roles (word w, keys k0 .. k0 + KPT - 1): K's
 // lanes run along the words of a key (its LDS rows are key-major), V's
@@ -65,15 +71,15 @@ __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_
 // Dequantization of one tile's raw words (this thread's keys) into the LDS
 // images: K as fp16 hi / lo rows, V^T as bf16 hi / lo (value s * n + b in
 // fp32, then its rounded high part and the rounded remainder).
-template <int D>
-__device__ __forceinline__ void pf_dequant(const PfRaw<D>& raw, _Float16* khi, _Float16* klo, __bf16* vthi,
+template <int D, bool F32>
+__device__ __forceinline__ void pf_dequant(const PfRaw<D, F32>& raw, _Float16* khi, _Float16* klo, __bf16* vthi,
                                            __bf16* vtlo, int w, int kb0, int wv, int kv0) {
   using Gm = PfGeom<D>;
   constexpr int KSTR = Gm::KSTR, VSTR = Gm::VSTR, KPT = Gm::KPT;
 #pragma unroll
   for (int e = 0; e < KPT; ++e) {
     const int key = kb0 + e;
-    const float ks = h2f(raw.ks[e]), kbias = h2f(raw.kb[e]);
+    const float ks = sbf(raw.ks[e]), kbias = sbf(raw.kb[e]);
     v8h kh, kl;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -92,7 +98,7 @@ __device__ __forceinline__ void pf_dequant(const PfRaw<D>& raw, _Float16* khi, _
     vkpt vh, vl;
 #pragma unroll
     for (int e = 0; e < KPT; ++e) {
-      const float x = fmaf(h2f(raw.vs[e]), static_cast<float>((raw.vw[e] >> (4 * j)) & 15u), h2f(raw.vb[e]));
+      const float x = fmaf(sbf(raw.vs[e]), static_cast<float>((raw.vw[e] >> (4 * j)) & 15u), sbf(raw.vb[e]));
       const __bf16 h = static_cast<__bf16>(x);
       vh[e] = h;
       vl[e] = static_cast<__bf16>(x - static_cast<float>(h));
@@ -102,26 +108,27 @@ __device__ __forceinline__ void pf_dequant(const PfRaw<D>& raw, _Float16* khi, _
   }
 }
 
-template <int D>
-__device__ __forceinline__ void pf_load(PfRaw<D>& R, const SdpaParams& p, int64_t row0, int t0,
+template <int D, bool F32>
+__device__ __forceinline__ void pf_load(PfRaw<D, F32>& R, const SdpaParams& p, int64_t row0, int t0,
                                         int last, int wk, int kk0, int wv, int kv0) {
   using Gm = PfGeom<D>;
+  using SB = typename PfRaw<D, F32>::SB;
 #pragma unroll
   for (int e = 0; e < Gm::KPT; ++e) {
     const int64_t rk = row0 + min(t0 + kk0 + e, last);
     const int64_t rv = row0 + min(t0 + kv0 + e, last);
     R.kw[e] = __builtin_nontemporal_load(p.kq + rk * Gm::W + wk);
     R.vw[e] = __builtin_nontemporal_load(p.vq + rv * Gm::W + wv);
-    R.ks[e] = static_cast<const uint16_t*>(p.ks)[rk * (D / 64) + (wk >> 3)];
-    R.kb[e] = static_cast<const uint16_t*>(p.kb)[rk * (D / 64) + (wk >> 3)];
-    R.vs[e] = static_cast<const uint16_t*>(p.vs)[rv * (D / 64) + (wv >> 3)];
-    R.vb[e] = static_cast<const uint16_t*>(p.vb)[rv * (D / 64) + (wv >> 3)];
+    R.ks[e] = static_cast<const SB*>(p.ks)[rk * (D / 64) + (wk >> 3)];
+    R.kb[e] = static_cast<const SB*>(p.kb)[rk * (D / 64) + (wk >> 3)];
+    R.vs[e] = static_cast<const SB*>(p.vs)[rv * (D / 64) + (wv >> 3)];
+    R.vb[e] = static_cast<const SB*>(p.vb)[rv * (D / 64) + (wv >> 3)];
   }
 }
 
 // D = 512: one wave per SIMD (q hi / lo and the O^T accumulators take 256
 // registers), 145 KB of LDS
-template <int D>
+template <int D, bool F32>
 __global__ __launch_bounds__(kPfThreads)
 __attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
 void prefill_int4_kernel(SdpaParams p) {
@@ -190,23 +197,23 @@ void prefill_int4_kernel(SdpaParams p) {
   // raw words of the tiles in flight: two (tiles it + 1 and it + 2 load
   // while tile it is computed), one at D = 512 (registers)
   constexpr int NB = D == 512 ? 1 : 2;
-  PfRaw<D> rawA, rawB;
-  pf_load<D>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
-  if constexpr (NB == 2) pf_load<D>(rawB, p, row0, min(lo + kPfKeys, last), last, w, kb0, wv, kv0);
+  PfRaw<D, F32> rawA, rawB;
+  pf_load<D, F32>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
+  if constexpr (NB == 2) pf_load<D, F32>(rawB, p, row0, min(lo + kPfKeys, last), last, w, kb0, wv, kv0);
 
   float m_run = -INFINITY, l_run = 0.0f;
   v4f o[DB];
 #pragma unroll
   for (int b = 0; b < DB; ++b) o[b] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto tile = [&](PfRaw<D>& raw, int it) {
+  auto tile = [&](PfRaw<D, F32>& raw, int it) {
     const int t0 = lo + it * kPfKeys;
     __syncthreads();  // every wave is done with the previous tile's LDS
     // ---- dequantize this thread's K / V words into LDS ----------------------
-    pf_dequant<D>(raw, khi, klo, vthi, vtlo, w, kb0, wv, kv0);
+    pf_dequant<D, F32>(raw, khi, klo, vthi, vtlo, w, kb0, wv, kv0);
     __syncthreads();
     // the words of tile it + NB go into this buffer while tiles it .. run
-    pf_load<D>(raw, p, row0, min(t0 + NB * kPfKeys, last), last, w, kb0, wv, kv0);
+    pf_load<D, F32>(raw, p, row0, min(t0 + NB * kPfKeys, last), last, w, kb0, wv, kv0);
 
     // ---- S^T = K q^T: two 16-key halves -----------------------------------
     float sc[8];
@@ -303,7 +310,7 @@ void prefill_int4_kernel(SdpaParams p) {
 // a step past the last tile dequantizes clamped rows, whose scores the
 // mask drops).  Two slots take 141 KB at D = 256, so D = 512 keeps the
 // kernel above.
-template <int D>
+template <int D, bool F32>
 __global__ __launch_bounds__(2 * kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_int4_ws_kernel(SdpaParams p) {
   pin_args(p);
@@ -337,14 +344,14 @@ void prefill_int4_ws_kernel(SdpaParams p) {
     constexpr int KB = kPfKeys / KPT;
     const int w = tid % W, kb0 = (tid / W) * KPT;
     const int wv = tid / KB, kv0 = (tid % KB) * KPT;
-    PfRaw<D> rawA, rawB;
-    pf_load<D>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
+    PfRaw<D, F32> rawA, rawB;
+    pf_load<D, F32>(rawA, p, row0, lo, last, w, kb0, wv, kv0);
     for (int st = 0; st < nt2; st += 2) {
-      pf_load<D>(rawB, p, row0, min(lo + (st + 1) * kPfKeys, last), last, w, kb0, wv, kv0);
-      pf_dequant<D>(rawA, khi[0], klo[0], vthi[0], vtlo[0], w, kb0, wv, kv0);
+      pf_load<D, F32>(rawB, p, row0, min(lo + (st + 1) * kPfKeys, last), last, w, kb0, wv, kv0);
+      pf_dequant<D, F32>(rawA, khi[0], klo[0], vthi[0], vtlo[0], w, kb0, wv, kv0);
       __syncthreads();
-      pf_load<D>(rawA, p, row0, min(lo + (st + 2) * kPfKeys, last), last, w, kb0, wv, kv0);
-      pf_dequant<D>(rawB, khi[1], klo[1], vthi[1], vtlo[1], w, kb0, wv, kv0);
+      pf_load<D, F32>(rawA, p, row0, min(lo + (st + 2) * kPfKeys, last), last, w, kb0, wv, kv0);
+      pf_dequant<D, F32>(rawB, khi[1], klo[1], vthi[1], vtlo[1], w, kb0, wv, kv0);
       __syncthreads();
     }
     __syncthreads();  // the compute waves' last tile
@@ -479,12 +486,21 @@ void prefill_int4_ws_kernel(SdpaParams p) {
   }
 }
 
+template <bool F32>
+void launch_tiles(const SdpaParams& p, int D, bool ws, dim3 grid, hipStream_t s) {
+  if (D == 128 && ws) prefill_int4_ws_kernel<128, F32><<<grid, 2 * kPfThreads, 0, s>>>(p);
+  else if (D == 256 && ws) prefill_int4_ws_kernel<256, F32><<<grid, 2 * kPfThreads, 0, s>>>(p);
+  else if (D == 128) prefill_int4_kernel<128, F32><<<grid, kPfThreads, 0, s>>>(p);
+  else if (D == 256) prefill_int4_kernel<256, F32><<<grid, kPfThreads, 0, s>>>(p);
+  else prefill_int4_kernel<512, F32><<<grid, kPfThreads, 0, s>>>(p);
+}
+
 }  // namespace
 
 // Returns -1 when the tile kernel does not serve the shape (the caller then
 // runs the split-K decode kernels in prefill mode).
 bool prefill_tiles_serve(int D, int sb_dtype, int gqa) {
-  if (sb_dtype != TQ_F16 || (D != 128 && D != 256 && D != 512)) return false;
+  if ((sb_dtype != TQ_F16 && sb_dtype != TQ_F32) || (D != 128 && D != 256 && D != 512)) return false;
   return gqa >= 1 && gqa <= kPfRows && kPfRows % gqa == 0;
 }
 
@@ -494,11 +510,8 @@ int launch_prefill_tiles(const SdpaParams& p, int D, int sb_dtype, hipStream_t s
   dim3 grid((p.nq + qpw - 1) / qpw, p.Hkv);
   // TQ_PREFILL_WS=0 selects the one-role kernel at D 128 / 256
   const bool ws = options().prefill_ws;
-  if (D == 128 && ws) prefill_int4_ws_kernel<128><<<grid, 2 * kPfThreads, 0, s>>>(p);
-  else if (D == 256 && ws) prefill_int4_ws_kernel<256><<<grid, 2 * kPfThreads, 0, s>>>(p);
-  else if (D == 128) prefill_int4_kernel<128><<<grid, kPfThreads, 0, s>>>(p);
-  else if (D == 256) prefill_int4_kernel<256><<<grid, kPfThreads, 0, s>>>(p);
-  else prefill_int4_kernel<512><<<grid, kPfThreads, 0, s>>>(p);
+  if (sb_dtype == TQ_F32) launch_tiles<true>(p, D, ws, grid, s);
+  else launch_tiles<false>(p, D, ws, grid, s);
   TQ_CHECK_LAUNCH("prefill_int4_kernel");
   return TQ_OK;
 }

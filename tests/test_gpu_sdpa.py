@@ -449,13 +449,18 @@ def test_sdpa_prefill_matches_oracle(gpu, Hq, Hkv, D, S, prior, W, qdt):
     (8, 1, 512, 70, 40, 64, "f16"),        # D 512 with a window, partial last group
     (16, 8, 512, 64, 10, 0, "f32"),        # D 512 GQA 2: 32 queries x 2 heads
 ])
-def test_sdpa_prefill_tile_kernel(gpu, Hq, Hkv, D, S, prior, W, qdt):
+@pytest.mark.parametrize("sb", ["f16", "f32"])
+def test_sdpa_prefill_tile_kernel(gpu, Hq, Hkv, D, S, prior, W, qdt, sb):
     """Prefills of >= 64 queries at D 128 / 256 / 512 run the K/V-tile kernel
-    (fp16 / bf16 hi-lo matrix-core products)."""
+    (fp16 / bf16 hi-lo matrix-core products), for fp16 and fp32 (the
+    reference's cache dtype) scale/bias."""
+    plan = gpu.sdpa_plan(Hq, Hkv, D, prior + S, mode="prefill", batch=S, sliding_window=W,
+                         sb_dtype=torch.float32 if sb == "f32" else torch.float16)
+    assert plan["kernel"] == ("prefill_int4_kernel" if D == 512 else "prefill_int4_ws_kernel")
     rng = np.random.default_rng(S * 7 + prior + Hq)
     cap = prior + S + 3
     qd, qv = queries(rng, (S, Hq, D), qdt)
-    c = host_cache(rng, Hkv, cap, D, "f16")
+    c = host_cache(rng, Hkv, cap, D, sb)
     out = gpu.sdpa_int4_prefill(qd, *[dev(a) for a in c], prior, Hq // Hkv, 1.0, W)
     ref = O.sdpa_int4_prefill(qv, *c, prior, Hq // Hkv, 1.0, W)
     assert_close(host(out), ref, f"tiles S{S} prior{prior} W{W} D{D} gqa{Hq // Hkv}")

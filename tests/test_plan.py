@@ -63,7 +63,9 @@ def test_sliding_and_prefill_plans():
     pf = tq.sdpa_plan(32, 16, 256, 4096, mode="prefill", batch=512, sliding_window=1024)
     assert pf["kernel"] == "prefill_int4_ws_kernel"
     pf32 = tq.sdpa_plan(32, 16, 256, 4096, mode="prefill", batch=512, sb_dtype=F32)
-    assert pf32["kernel"] in ("prefill_int4_ws_kernel", "sdpa_int4_mfma_kernel")
+    assert pf32["kernel"] == "prefill_int4_ws_kernel"
+    g32 = tq.sdpa_plan(32, 4, 512, 4096, mode="prefill", batch=512, sb_dtype=F32)
+    assert g32["kernel"] == "prefill_int4_kernel"
 
 
 def test_plan_rejects_bad_arguments():
