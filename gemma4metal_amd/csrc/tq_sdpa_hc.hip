@@ -672,8 +672,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     for (int blk = 0; blk < 4; ++blk) wsum[blk] = bacc[blk] = 0.0f;
 
     // One step: this step's products, with the next step's K and scale
-    // loads issued among them (scales first, then two K loads per pair), so
-    // the wave never stalls on a burst of loads after the barrier.
+    // loads issued among them (scales first, then the K loads of two pairs
+    // after each even pair), so the wave never stalls on a burst of loads
+    // after the barrier.
     auto produce = [&](const uint32_t (&kw)[2][16], const u32x4 (&scw)[2][SW], int st, uint32_t (&nk)[2][16],
                        u32x4 (&ns)[2][SW]) {
       const int t0 = base0 + st * kIter, slot = st & 1;
@@ -742,9 +743,15 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
             sc[tile][i] = fmaf(dot, ks[i], fmaf(kb[i], qh[P], sc[tile][i]));
           }
         }
-        __builtin_amdgcn_sched_barrier(0);
-        hc_load_kw_pair(nk, kq_rows, tn, safe_last - tn, m, c, P);
-        __builtin_amdgcn_sched_barrier(0);
+        // pairs 2P', 2P' + 1 together: the two 64-byte halves of each
+        // 128-byte line go out in one batch (apart, the non-temporal line
+        // was fetched twice: 1.16x the algorithmic bytes)
+        if ((P & 1) == 0) {
+          __builtin_amdgcn_sched_barrier(0);
+          hc_load_kw_pair(nk, kq_rows, tn, safe_last - tn, m, c, P);
+          hc_load_kw_pair(nk, kq_rows, tn, safe_last - tn, m, c, P + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile)
@@ -850,7 +857,7 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
     asm volatile("" : "+v"(magic));
 
     // One step: this step's products, with the next step's V loads issued
-    // among them (two per block).
+    // among them (four after each even block).
     auto consume = [&](const u32x4 (&vr)[2][4], int st, u32x4 (&nx)[2][4]) {
       const int tn = tclamp(base0 + (st + 1) * kIter);
       const int slot = st & 1;
@@ -871,9 +878,12 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) vw[4 * T + i] = t[i];
         }
-        __builtin_amdgcn_sched_barrier(0);
-        hc_load_v4_blk(nx, vq_rows, tn, safe_last - tn, m, c, blk);
-        __builtin_amdgcn_sched_barrier(0);
+        if ((blk & 1) == 0) {  // both halves of each 128-byte line at once
+          __builtin_amdgcn_sched_barrier(0);
+          hc_load_v4_blk(nx, vq_rows, tn, safe_last - tn, m, c, blk);
+          hc_load_v4_blk(nx, vq_rows, tn, safe_last - tn, m, c, blk + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
         const uint4* src = pv_lds + (((slot * NS + s) * 4 + blk) * 2) * 64 + lane;
         const v8bf bhi = __builtin_bit_cast(v8bf, src[0]);
         const v8bf blo = __builtin_bit_cast(v8bf, src[64]);
