@@ -81,7 +81,7 @@ def gen_cache(tq, torch, Hkv, L, D, gen, cap=None, sb=None):
 def precision_note(sb_name):
     """The arithmetic of the matrix-core decode kernel, stated in full."""
     return (f"int4 K/V ({sb_name} scale/bias), bf16 Q; K.q on int8 matrix cores with q as "
-            "22-bit fixed point per head (exact integer dot per quant group), P.V on bf16 "
+            "22-bit (D 512: 21-bit) fixed point per head (exact integer dot per quant group), P.V on bf16 "
             "matrix cores with the weights p*s_v split into bf16 hi+lo (~16-bit mantissa), "
             "fp32 accumulate and softmax")
 
