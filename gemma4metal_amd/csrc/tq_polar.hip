@@ -1010,18 +1010,36 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
   // rotated level-1 rows (p7_t1_row): row jj of quarter qt is at
   // 16 qt + (jj & ~3) + ((jj + qt) & 3)
   const char* t1b = reinterpret_cast<const char*>(&T.t1[0][0][0]) + qt * (16 * 16 * kE);
-  uint32_t rot[4];
+  const char* t1r[4];  // rotated row base of pair jj with jj % 4 == e
 #pragma unroll
-  for (int e = 0; e < 4; ++e) rot[e] = static_cast<uint32_t>((e + qt) & 3) * (16 * kE);
+  for (int e = 0; e < 4; ++e) t1r[e] = t1b + static_cast<uint32_t>((e + qt) & 3) * (16 * kE);
+  // entry offsets nibble * kE (at most 15 * 16 = 240) pre-scaled into bytes:
+  // byte b of lo[w] / hi[w] is the low / high nibble of byte b of word w
+  // times kE, so each lookup address is one add of a selected byte
+  constexpr int kSh = kE == 4 ? 2 : (kE == 8 ? 3 : 4);
+  constexpr uint32_t kMask = 0x0F0F0F0Fu << kSh;
+  uint32_t lo[2], hi[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    lo[w] = (Q.l1[w] << kSh) & kMask;
+    hi[w] = (Q.l1[w] >> (4 - kSh)) & kMask;
+    // opaque: otherwise each byte select is folded back into a shift and a
+    // mask of the raw word (two instructions per lookup instead of none)
+    asm("" : "+v"(lo[w]), "+v"(hi[w]));
+  }
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
     const float r1[4] = {r3[ii] * tc[ii].x, r3[ii] * tc[ii].y, r3[ii] * tc[ii].z, r3[ii] * tc[ii].w};
-    const uint32_t word = Q.l1[ii >> 1];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int jj = 4 * ii + e;  // level-1 pair 16 qt + jj
-      const uint32_t nib = __builtin_amdgcn_ubfe(word, 4 * (jj % 8), 4);
-      const float* ent = reinterpret_cast<const float*>(t1b + ii * (4 * 16 * kE) + rot[e] + nib * kE);
+      const int jj = 4 * ii + e;  // level-1 pair 16 qt + jj: nibble jj % 8 of word jj / 8
+      const int n = jj % 8;
+      const uint32_t src = (n & 1) ? hi[jj >> 3] : lo[jj >> 3];
+      const uint32_t off = (src >> (8 * (n >> 1))) & 0xFFu;
+      // one aligned G-float read (ds_read_b64 at G = 2, with the constant in
+      // its offset field)
+      typedef float vGf __attribute__((ext_vector_type(G)));
+      const vGf ent = *reinterpret_cast<const vGf*>(t1r[e] + ii * (4 * 16 * kE) + off);
 #pragma unroll
       for (int g = 0; g < G; ++g) acc[g] = fmaf(r1[e], ent[g], acc[g]);
     }
