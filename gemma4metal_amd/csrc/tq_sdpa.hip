@@ -212,6 +212,20 @@ SdpaPlan plan_sdpa(int mode, int batch, int Hq, int Hkv, int D, int max_len, int
     pl.kernel = SdpaKernel::mfma;
   else
     pl.kernel = SdpaKernel::valu;
+  // Ragged batches of up to 64 sequences on the matrix-core kernel choose
+  // their chunk on the device (ragged_job), among 1 .. max_splits chunks of
+  // the longest sequence.  Every sequence is at least one job, so with two
+  // or more workgroups' worth of (sequence, head) jobs per CU the grid
+  // allows at most two chunks per sequence: fewer grid workgroups then go
+  // without a job (each still costs its CU a dispatch and a load of the
+  // lengths).
+  pl.lpt = mode == 1 && batch <= 64 && pl.kernel == SdpaKernel::mfma;
+  if (pl.lpt && groups >= 2 * static_cast<int64_t>(target_wgs()) && pl.max_splits > 2) {
+    pl.max_splits = 2;
+    const int64_t half = (static_cast<int64_t>(eff_len) + 1) / 2;
+    pl.chunk = std::max<int>(pl.chunk, static_cast<int>((half + kChunkGranule - 1) / kChunkGranule * kChunkGranule));
+    pl.wl = ws_layout(batch, Hq, D, pl.max_splits);
+  }
   return pl;
 }
 
@@ -543,6 +557,11 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   p.prefill = prefill;
   p.pq = pq;
   p.nq = batch;
+  // ragged batches of up to 64 sequences on the matrix-core kernel: chunk
+  // chosen on the device from the lengths, longest-first workgroup order
+  // (ragged_job); the grid and workspace stay sized for pl.max_splits
+  p.lpt = pl.lpt ? 1 : 0;
+  p.cus = target_wgs();
 
   dim3 grid(max_splits, Hkv * n_sub, (batch + pq - 1) / pq);
   hipStream_t s = static_cast<hipStream_t>(stream);

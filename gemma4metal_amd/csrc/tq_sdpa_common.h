@@ -55,6 +55,11 @@ struct SdpaParams {
   // queries (grid z = query groups) of its heads, nq queries in all.
   int pq;
   int nq;
+  // Ragged launches of at most 64 sequences: the chunk is chosen on the
+  // device from the lengths, and workgroups take their (sequence, split)
+  // from the longest-first order of ragged_job.  cus: compute units.
+  int lpt;
+  int cus;
 };
 
 // Kernel arguments arrive through scalar loads from the kernarg segment, one
@@ -94,6 +99,93 @@ __device__ __forceinline__ SplitRange split_range(const SdpaParams& p, int b, in
   r.t_begin = lo + split * p.chunk;
   r.t_end = min(r.t_begin + p.chunk, n_b);
   return r;
+}
+
+// Job of a workgroup in a ragged launch with p.lpt set (at most 64
+// sequences).
+// - The chunk is chosen here, from the actual lengths (the host knows only
+//   the longest, and sizes the grid and workspace for p.max_splits chunks
+//   of it): of the candidates ceil(Lmax / k) (rounded up to 128 keys),
+//   k = 1 .. p.max_splits, the one with the least estimated makespan
+//   max(F + c, (F * jobs(c) + keys) / CUs), F = kLptFixedKeys, a
+//   workgroup's fixed cost (prologue, split merge) in keys streamed.  One
+//   chunk per sequence (no merge) wins when many sequences fill the chip;
+//   a few long sequences among short ones get split.
+// - The (sequence, kv-head column, split) cells then run in longest-first
+//   order, so that the chunks that take longest start first and the launch
+//   does not end on a few long chunks dispatched last: all full chunks
+//   first (sequence, then split order), then each sequence's last, partial
+//   chunk by size, largest first (ties: lower sequence first); the heads
+//   of one cell are consecutive.
+// Every wave computes the same mapping from one load of the lengths (lane
+// i: sequence i), so no barrier is needed.  A job's work and its split
+// merge order do not depend on which workgroup runs it.  Returns false for
+// a workgroup beyond the last job.
+constexpr int kLptFixedKeys = 870;
+
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) v = max(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+__device__ __forceinline__ bool ragged_job(const SdpaParams& p, int& b, int& hy, int& split, int& chunk) {
+  const int lane = threadIdx.x & 63;
+  const int H = static_cast<int>(gridDim.y);
+  const int64_t wg = blockIdx.x + static_cast<int64_t>(gridDim.x) * (blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z);
+  const bool mine = lane < p.nq;
+  const int n_b = mine ? min(p.seq_lens[lane], p.n_clamp) : 0;
+  const int W = mine ? (p.windows ? p.windows[lane] : p.window) : 0;
+  const int lo = W > 0 ? max(0, n_b - W) : 0;
+  const int len = max(n_b - lo, 0);
+  // ---- chunk: candidates k = 1 .. max_splits, one wave-wide job count each
+  const int lmax = wave_max_i(len);
+  const float keys = static_cast<float>(wave_sum_dpp(len)) * H;
+  const float cus = static_cast<float>(max(p.cus, 1));
+  float best = INFINITY;
+  chunk = p.chunk;
+  for (int k = 1; k <= p.max_splits; ++k) {  // uniform loop
+    const int cand = max(128, ((lmax + k - 1) / k + 127) / 128 * 128);
+    const int jobs = wave_sum_dpp(mine ? (len > 0 ? (len + cand - 1) / cand : 1) : 0);
+    const float est = fmaxf(static_cast<float>(kLptFixedKeys + cand),
+                            (static_cast<float>(kLptFixedKeys) * jobs * H + keys) / cus);
+    if (est < best) {  // uniform: strictly better, so ties keep the smaller k
+      best = est;
+      chunk = cand;
+    }
+  }
+  // ---- longest-first order ------------------------------------------------------
+  const int full = mine ? len / chunk : 0;
+  const int rem = len - full * chunk;
+  const bool part = mine && (rem > 0 || len == 0);  // one partial (or empty) chunk
+  const int F = wave_sum_dpp(full);  // full chunks in all
+  const int64_t r = wg / H;
+  hy = static_cast<int>(wg - r * H);
+  if (r >= F + static_cast<int>(__builtin_popcountll(__ballot(part)))) return false;  // no job
+  if (r < F) {
+    // inclusive prefix sum of the full-chunk counts over the lanes
+    int pre = full;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(pre, d, 64);
+      if (lane >= d) pre += v;
+    }
+    const uint64_t m = __ballot(pre > r);
+    b = __builtin_ffsll(static_cast<long long>(m)) - 1;
+    split = static_cast<int>(r) - (__builtin_amdgcn_readlane(pre, b) - __builtin_amdgcn_readlane(full, b));
+    return true;
+  }
+  // rank of this lane's partial chunk among all partial chunks
+  int rank = 0;
+  for (int j = 0; j < 64; ++j) {
+    const int rj = __builtin_amdgcn_readlane(rem, j);
+    const bool pj = __builtin_amdgcn_readlane(static_cast<int>(part), j) != 0;
+    rank += (pj && (rj > rem || (rj == rem && j < lane))) ? 1 : 0;
+  }
+  const uint64_t m = __ballot(part && rank == static_cast<int>(r - F));
+  b = __builtin_ffsll(static_cast<long long>(m)) - 1;
+  split = __builtin_amdgcn_readlane(full, b);
+  return true;
 }
 
 // Key range of the prefill query group b0 .. b_last (positions n + b0 ..):
@@ -360,6 +452,7 @@ struct SdpaPlan {
   int chunk;       // keys per split
   int max_splits;  // grid.x: bound of the splits of any sequence
   WsLayout wl;     // workspace layout
+  bool lpt;        // ragged: device-chosen chunk, longest-first order (ragged_job)
 };
 // mode: 0 single sequence (n = kv_len), 1 ragged batch (max_len bounds the
 // lengths), 2 prefill (batch = queries, max_len = n_prior + n_new).

@@ -187,7 +187,12 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int T = PACK ? (m >> 3) : 0;
   const int hn = n / NG, gn = n - (n / NG) * NG;
   const bool col_used = n < COLS;
-  const int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
+  if (!kQG && p.lpt) {
+    int chunk = p.chunk;
+    if (!ragged_job(p, b, hy, split, chunk)) return;
+    p.chunk = chunk;  // this launch's chunk, chosen from the lengths
+  }
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
   // The G column sets are GH heads x pq queries: pq = 1 unless kQG (b is
   // then the query group of queries b0 .. b_last).

@@ -135,6 +135,41 @@ def test_ragged_batch_matches_oracle(gpu, sb):
     assert_close(host(out), ref, "ragged")
 
 
+@pytest.mark.parametrize("long_len,W", [(20000, 0), (9000, 4096)])
+def test_ragged_skewed_batch(gpu, long_len, W):
+    """One long sequence among 63 short ones: the device chooses its own
+    chunk for the batch (the long sequence split, the short ones whole)
+    and runs the jobs longest first; every sequence matches the oracle.
+    The cache is quantized on the GPU, row range by row range."""
+    from oracle import coracle
+    rng = np.random.default_rng(long_len + W)
+    B, Hq, Hkv, D = 64, 32, 16, 256
+    cap = long_len + 1
+    lens = np.concatenate([[long_len], rng.integers(1, 600, size=B - 1)]).astype(np.int32)
+    wins = np.full(B, W, np.int32)
+    g = torch.Generator(device="cuda").manual_seed(long_len)
+    kq = torch.zeros((B, Hkv, cap, D // 8), dtype=torch.uint32, device="cuda")
+    vq = torch.zeros_like(kq)
+    ks = torch.zeros((B, Hkv, cap, D // 64), dtype=torch.float16, device="cuda")
+    kb, vs, vb = torch.zeros_like(ks), torch.zeros_like(ks), torch.zeros_like(ks)
+    for b in range(B):
+        n = int(lens[b])
+        for h in range(Hkv):
+            k = torch.randn((n, D), generator=g, device="cuda")
+            k = k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)
+            v = torch.randn((n, D), generator=g, device="cuda")
+            kq[b, h, :n], ks[b, h, :n], kb[b, h, :n] = gpu.quantize(k, scale_dtype=torch.float16)
+            vq[b, h, :n], vs[b, h, :n], vb[b, h, :n] = gpu.quantize(v, scale_dtype=torch.float16)
+    qd, qv = queries(rng, (B, Hq, D), "bf16")
+    out = host(gpu.sdpa_int4_ragged(qd, kq, ks, kb, vq, vs, vb, dev(lens), Hq // Hkv,
+                                    windows=dev(wins)))
+    for b in range(B):
+        n = int(lens[b])
+        cb = [host(x[b, :, :n]) for x in (kq, ks, kb, vq, vs, vb)]
+        ref = coracle.sdpa_int4_f64(qv[b], *cb, Hq // Hkv, 1.0, W)
+        assert_close(out[b], ref, f"sequence {b} (L={n})")
+
+
 def test_append_then_attend_round_trip(gpu):
     """Config-4 step at reduced size: quantize+append one fp32 token per
     sequence, then ragged decode over the grown caches."""

@@ -74,3 +74,13 @@ def test_plan_rejects_bad_arguments():
         tq.sdpa_plan(32, 16, 96, 100)
     with pytest.raises(TQError):
         tq.sdpa_plan(30, 16, 256, 100)
+
+
+def test_ragged_plan_bounds_the_device_chunk():
+    # ragged batches of up to 64 sequences choose their chunk on the device
+    # (1 .. splits chunks of the longest); with >= 2 (sequence, head) jobs
+    # per CU the grid allows at most two
+    pl = tq.sdpa_plan(32, 16, 256, 32769, mode="ragged", batch=64)
+    assert pl["splits"] == 2 and pl["chunk"] >= (32769 + 1) // 2
+    small = tq.sdpa_plan(32, 16, 256, 32769, mode="ragged", batch=8)
+    assert small["splits"] == 5
