@@ -127,9 +127,11 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// v of lane l ^ 8 within each row of 16 lanes (DPP row_ror:8).
+// v of lane l ^ 8 within each row of 16 lanes (DPP row_ror:8).  Every lane
+// reads a lane of its own row, so no old value is needed (mov_dpp: no
+// register initialised for lanes without a source).
 __device__ __forceinline__ float ror8(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
 }
 
 // The same butterfly as a max over aligned groups of 16 lanes.

@@ -170,13 +170,14 @@ WsLayout ws_layout(int batch, int Hq, int D, int max_splits) {
 // - Prefill of >= 64 queries: the K/V-tile kernels where they serve.
 // - The VALU kernel under TQ_SDPA_IMPL=valu.
 SdpaPlan plan_sdpa(int mode, int batch, int Hq, int Hkv, int D, int max_len, int gqa, int window,
-                   int sb_dtype) {
+                   int sb_dtype, int cap) {
   (void)Hq;
   const Options o = options();
   const bool prefill = mode == 2;
-  const bool try_mfma = !o.sdpa_valu;
   SdpaPlan pl{};
-  const bool hc = try_mfma && D == 512 && gqa % 8 == 0 && hc_serves(sb_dtype);
+  const bool hc = !o.sdpa_valu && D == 512 && gqa % 8 == 0 && hc_serves(sb_dtype);
+  // the matrix-core kernel reads whole 32-row blocks of the cache
+  const bool try_mfma = !o.sdpa_valu && cap >= kMfmaMinRows;
   int G = head_subgroup(gqa);
   // the matrix-core kernel takes at most 16 (head, quant group) columns:
   // halve the head subgroup until it serves the shape
@@ -520,7 +521,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
 
   const int mode = prefill ? 2 : (seq_lens ? 1 : 0);
-  const SdpaPlan pl = plan_sdpa(mode, batch, Hq, Hkv, D, max_len, gqa, window, sb_dtype);
+  const SdpaPlan pl = plan_sdpa(mode, batch, Hq, Hkv, D, max_len, gqa, window, sb_dtype, cap);
   const int n_sub = pl.n_sub, pq = pl.pq, max_splits = pl.max_splits;
   const WsLayout wl = pl.wl;
   if (max_splits > 1) {
@@ -616,7 +617,7 @@ extern "C" int tq_sdpa_int4_plan(int mode, int batch, int num_heads, int num_kv_
                    num_heads % num_kv_heads == 0 && max_kv_len >= 0 && sliding_window >= 0,
                "%s: bad shape", fn);
   const SdpaPlan pl = plan_sdpa(mode, batch, num_heads, num_kv_heads, head_dim, max_kv_len,
-                                num_heads / num_kv_heads, sliding_window, sb_dtype);
+                                num_heads / num_kv_heads, sliding_window, sb_dtype, max_kv_len);
   if (splits) *splits = pl.max_splits;
   if (chunk_keys) *chunk_keys = pl.chunk;
   if (kernel && kernel_bytes > 0) {
@@ -694,7 +695,7 @@ extern "C" int tq_sdpa_int4_noalloc(const void* q, tq_dtype q_dtype, const uint3
       gqa_factor >= 1 && num_heads == num_kv_heads * gqa_factor && kv_len >= 0 &&
       sliding_window >= 0 && (sb_dtype == TQ_F16 || sb_dtype == TQ_F32)) {
     const SdpaPlan pl = plan_sdpa(0, 1, num_heads, num_kv_heads, head_dim, kv_len, gqa_factor,
-                                  sliding_window, sb_dtype);
+                                  sliding_window, sb_dtype, kv_capacity);
     if (pl.max_splits > 1 && pl.wl.total > kScratchBytes) {
       set_error("%s: this shape needs %zu bytes of split-K scratch, more than the library's "
                 "static %zu bytes; call tq_sdpa_int4 with a workspace instead",

@@ -455,9 +455,13 @@ struct SdpaPlan {
   bool lpt;        // ragged: device-chosen chunk, longest-first order (ragged_job)
 };
 // mode: 0 single sequence (n = kv_len), 1 ragged batch (max_len bounds the
-// lengths), 2 prefill (batch = queries, max_len = n_prior + n_new).
+// lengths), 2 prefill (batch = queries, max_len = n_prior + n_new); cap =
+// the cache's rows per (sequence, kv head).
 SdpaPlan plan_sdpa(int mode, int batch, int Hq, int Hkv, int D, int max_len, int gqa, int window,
-                   int sb_dtype);
+                   int sb_dtype, int cap);
+// Smallest cache capacity (rows) the matrix-core kernel serves: it reads
+// whole 32-row blocks.
+constexpr int kMfmaMinRows = 32;
 const char* kernel_name(const SdpaPlan& pl, int D, int sb_dtype);
 
 // (D, query columns) served by the matrix-core kernel, for a scale dtype.

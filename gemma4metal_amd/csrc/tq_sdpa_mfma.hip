@@ -22,7 +22,8 @@
 // Lane roles (l = lane, m = l % 16, c = l / 16; layouts checked on hardware):
 //   A rows / B cols / C cols = m;  k-slot j of lane-group c is k = 8c + j
 //   (bf16) or 16c + 4v + byte (i8);  C rows held by lane-group c: 4c .. 4c+3.
-//   Key of V slot j in lane-group c: t0 + 16*(j/4) + 4c + (j%4), which is the
+//   Key of V slot j in lane-group c: r0 + 16*(j/4) + 4c + (j%4) (r0 = first
+//   row of the iteration's 32-row block), which is the
 //   K tile (j/4), C row 4c + (j%4): the softmax weights are produced by the
 //   K MFMAs exactly in the lanes and slots the V MFMAs consume them from.
 //
@@ -42,6 +43,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 template <int D, int G, bool F32>
 struct MGeom {
@@ -70,16 +72,17 @@ struct MGeom {
 
 template <int D, bool F32>
 struct IterBuf {
-  uint32_t kw[2][D / 32];   // [tile][word] K slice of key (t0 + 16*tile + m)
+  uint32_t kw[2][D / 32];   // [tile][word] K slice of key (r0 + 16*tile + m)
   uint32_t vw[8][D / 128 / (D == 512 ? 2 : 1)];  // [slot][word] this wave's V words of key(slot)
-  uint32_t sc[2][F32 ? D / 64 : D / 128];  // scales of keys (t0 + 2k, t0 + 2k + 1) of array l/16
+  uint32_t sc[2][F32 ? D / 64 : D / 128];  // scales of keys (r0 + 2k, r0 + 2k + 1) of array l/16
 };
 
-// Per-lane row offsets (in keys) inside one 32-key iteration.
-struct LaneRows {
-  int k[2];   // K rows of tiles 0, 1
-  int v[8];   // V rows of slots 0..7
-  int s[2];   // scale rows of this lane's key pair
+// Per-lane byte offsets inside one 32-key block, from its first row: K row
+// m (tile 0; tile 1 adds 16 rows), V row 4c (slot j adds 16 * (j / 4) +
+// j % 4 rows), and this lane's scale key pair.  Constant over the stream:
+// an iteration moves the uniform block base only.
+struct LaneOffs {
+  uint32_t k, v, s;
 };
 
 // One streamed load: non-temporal when kNT (single sequences: ~7% more HBM
@@ -91,58 +94,58 @@ __device__ __forceinline__ T stream_load(const T* p) {
   else return *p;
 }
 
-// Loads of one iteration starting at key t0: every row index is clamped to
-// `last` with one v_min against a uniform limit (only the final, partial
-// iteration of a wave is affected), and addressed as a uniform base plus a
-// 32-bit lane offset.
+// Loads of the 32-row block starting at row `r0` (uniform): each load is
+// the block's base (scalar registers) plus a constant lane offset and an
+// immediate row offset, so an iteration spends no vector instructions on
+// addresses.  The caller keeps rows r0 .. r0 + 31 inside the cache
+// (block_row).
 template <int D, int G, bool F32, bool kNT>
 __device__ __forceinline__ void load_iter(IterBuf<D, F32>& B, const uint32_t* kq_row0,
                                           const uint32_t* vq_row0, const uint32_t* sc_arr,
-                                          const LaneRows& lr, int t0, int last, int m, int c,
-                                          int vhalf) {
+                                          const LaneOffs& lo, int r0) {
   using Gm = MGeom<D, G, F32>;
   constexpr uint32_t RB = D / 2;  // bytes per packed row
-  const int lim = last - t0;      // uniform; >= 0 for every issued iteration
-  const char* kb = reinterpret_cast<const char*>(kq_row0 + static_cast<int64_t>(t0) * (D / 8));
-  const char* vb = reinterpret_cast<const char*>(vq_row0 + static_cast<int64_t>(t0) * (D / 8));
-  const char* sb = reinterpret_cast<const char*>(sc_arr + static_cast<int64_t>(t0) * Gm::SCW);
+  // (uniform base + zero-extended lane offset, then the constant row offset
+  // as a separate addition: the form the compiler folds into the
+  // instruction's scalar base, vector offset and immediate)
+  const char* kb = reinterpret_cast<const char*>(kq_row0 + static_cast<int64_t>(r0) * (D / 8)) + lo.k;
+  const char* vb = reinterpret_cast<const char*>(vq_row0 + static_cast<int64_t>(r0) * (D / 8)) + lo.v;
+  const char* sb = reinterpret_cast<const char*>(sc_arr + static_cast<int64_t>(r0) * Gm::SCW) + lo.s;
 #pragma unroll
   for (int tile = 0; tile < 2; ++tile) {
-    const uint32_t off = static_cast<uint32_t>(min(lr.k[tile], lim)) * RB + c * Gm::KW * 4;
 #pragma unroll
     for (int w = 0; w < Gm::KW; w += 4) {
-      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(kb + off + w * 4));
+      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(kb + (tile * 16 * RB + w * 4)));
       B.kw[tile][w] = u.x; B.kw[tile][w + 1] = u.y; B.kw[tile][w + 2] = u.z; B.kw[tile][w + 3] = u.w;
     }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t off = static_cast<uint32_t>(min(lr.v[j], lim)) * RB +
-                         (m * Gm::VW + vhalf * Gm::VWH) * 4;
+    const char* a = vb + (16 * (j >> 2) + (j & 3)) * RB;
     if constexpr (Gm::VWH == 4) {
-      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(vb + off));
+      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(a));
       B.vw[j][0] = u.x; B.vw[j][1] = u.y; B.vw[j][2] = u.z; B.vw[j][3] = u.w;
     } else if constexpr (Gm::VWH == 2) {
-      const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(vb + off));
+      const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(a));
       B.vw[j][0] = u.x; B.vw[j][1] = u.y;
     } else {
-      B.vw[j][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(vb + off));
+      B.vw[j][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(a));
     }
   }
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const uint32_t off = static_cast<uint32_t>(min(lr.s[e], lim)) * (Gm::SCW * 4);
+    const char* a = sb + e * (Gm::SCW * 4);
     if constexpr (Gm::SCW >= 4) {
 #pragma unroll
       for (int w = 0; w < Gm::SCW; w += 4) {
-        const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(sb + off + 4 * w));
+        const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(a + 4 * w));
         B.sc[e][w] = u.x; B.sc[e][w + 1] = u.y; B.sc[e][w + 2] = u.z; B.sc[e][w + 3] = u.w;
       }
     } else if constexpr (Gm::SCW == 2) {
-      const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(sb + off));
+      const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(a));
       B.sc[e][0] = u.x; B.sc[e][1] = u.y;
     } else {
-      B.sc[e][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(sb + off));
+      B.sc[e][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(a));
     }
   }
 }
@@ -188,10 +191,21 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int hn = n / NG, gn = n - (n / NG) * NG;
   const bool col_used = n < COLS;
   int b = blockIdx.z, hy = blockIdx.y, split = blockIdx.x;
-  if (!kQG && p.lpt) {
-    int chunk = p.chunk;
-    if (!ragged_job(p, b, hy, split, chunk)) return;
-    p.chunk = chunk;  // this launch's chunk, chosen from the lengths
+  // Longest-first ragged order: batched launches only (single-sequence and
+  // grouped-prefill launches never set lpt).
+  if constexpr (!kQG && !kStreamNT) {
+    if (p.lpt) {
+      int chunk = p.chunk;
+      const bool job = ragged_job(p, b, hy, split, chunk);
+      // Every lane computes the same job; read back as wave-uniform values
+      // so that the split range, the key offsets and the load addresses
+      // derived from them stay in scalar registers.
+      if (!__builtin_amdgcn_readfirstlane(job)) return;
+      b = __builtin_amdgcn_readfirstlane(b);
+      hy = __builtin_amdgcn_readfirstlane(hy);
+      split = __builtin_amdgcn_readfirstlane(split);
+      p.chunk = __builtin_amdgcn_readfirstlane(chunk);  // this launch's chunk, chosen from the lengths
+    }
   }
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
   // The G column sets are GH heads x pq queries: pq = 1 unless kQG (b is
@@ -235,20 +249,22 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int arr = lane >> 4, k16 = lane & 15;  // this lane's scale array / key pair
   const void* sc_base = arr == 0 ? p.ks : (arr == 1 ? p.kb : (arr == 2 ? p.vs : p.vb));
   const uint32_t* sc_arr = static_cast<const uint32_t*>(sc_base) + row0 * Gm::SCW;
-  LaneRows lr;
-  lr.k[0] = m;
-  lr.k[1] = 16 + m;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) lr.v[j] = 16 * (j >> 2) + 4 * c + (j & 3);
-  lr.s[0] = 2 * k16;
-  lr.s[1] = 2 * k16 + 1;
-
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   // wave wv streams keys with the NWK waves of its V half (wv / NWK)
   const int vhalf = wv / NWK;
+  LaneOffs lo;
+  lo.k = m * (D / 2) + c * Gm::KW * 4;
+  lo.v = 4 * c * (D / 2) + (m * Gm::VW + vhalf * Gm::VWH) * 4;
+  lo.s = 2 * k16 * Gm::SCW * 4;
   const int base0 = t_begin + (wv - vhalf * NWK) * 32;
   const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
-  const int last = t_end - 1;
+  // First row of the 32-row block read for the iteration at key t0: t0
+  // itself while the block lies below t_end; else moved back to end at
+  // t_end (rows of the split, the keys before t0 masked in process), and to
+  // row 0 for splits ending before row 32.  Rows stay in [0, max(t_end,
+  // 32)), inside the cache: the planner gives this kernel capacities of at
+  // least 32 rows.  Wave-uniform (scalar).
+  auto block_row = [&](int t0) { return max(0, min(t0, t_end - 32)); };
 
   // q is loaded first: at kernel start every workgroup issues its K/V stream
   // at once, and the prologue (which needs only q) should not wait for it.
@@ -272,13 +288,10 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   }
   __builtin_amdgcn_sched_barrier(0);
   // Issued unconditionally (a load under a branch makes the compiler drain
-  // every outstanding load at the join): rows are clamped into
-  // [0, max(last, 0)], valid memory even for a wave or split with no keys
-  // (capacity >= 1).
+  // every outstanding load at the join): block_row keeps the rows of a wave
+  // or split with no keys inside the cache.
   IterBuf<D, F32> bufA, bufB;
-  const int safe_last = max(last, 0);
-  load_iter<D, G, F32, kStreamNT>(bufA, kq_row0, vq_row0, sc_arr, lr, min(base0, safe_last), safe_last, m, c,
-                  vhalf);
+  load_iter<D, G, F32, kStreamNT>(bufA, kq_row0, vq_row0, sc_arr, lo, block_row(base0));
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue: q as 22-bit fixed point per head, B operands via LDS ------
@@ -372,6 +385,10 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   };
 
   auto process = [&](const IterBuf<D, F32>& B, int t0) {
+    // B holds the block of rows r0 .. r0 + 31 (r0 <= t0); its keys below t0
+    // or from t_end on are masked
+    const int r0 = block_row(t0);
+    const uint32_t n_keep = static_cast<uint32_t>(t_end - t0);  // > 0 for a processed iteration
     // scales -> LDS [array][group][key]
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -389,7 +406,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // K . q on the int8 matrix cores.  Score slot 4*u + i of this lane is key
-    // t0 + 16*tile(u) + 4c + i of column n: tile(u) = T with packed columns
+    // r0 + 16*tile(u) + 4c + i of column n: tile(u) = T with packed columns
     // (one score tile), u otherwise (two).
     constexpr int NU = PACK ? 1 : 2;
     float sc[4 * NU];
@@ -412,6 +429,10 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         }
       }
     };
+    // With packed columns (every lane's column used) and no per-column
+    // limits, a block whose 32 rows all lie in [t0, t_end) needs no mask.
+    constexpr bool kMaskAll = !PACK || kQG;
+    const bool full = r0 == t0 && n_keep >= 32;  // uniform
     auto scores = [&](const v4i (&acc)[3], int u, int tile) {
       const v4f ks = scale4(0, gn, tile), kb = scale4(1, gn, tile);
 #pragma unroll
@@ -419,12 +440,28 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         // digits 0 and 1 combine exactly in int32 (|.| < 2^25)
         const int lo01 = acc[0][i] + (acc[1][i] << 8);
         const float dot = static_cast<float>(lo01) + 65536.0f * static_cast<float>(acc[2][i]);
-        float part = dot * (ks[i] * sf) + kb[i] * qhat;
+        // (fma with + 0: the fp16 scale converts inside the multiply)
+        const float kss = fmaf(ks[i], sf, 0.0f), kbq = fmaf(kb[i], qhat, 0.0f);
+        float part = fmaf(dot, kss, kbq);
         part = group_sum<NG>(part);
-        const int t = t0 + 16 * tile + 4 * c + i;
-        bool keep = t < t_end && col_used;
-        if constexpr (kQG) keep = keep && t <= col_hi && t >= col_lo;
-        sc[4 * u + i] = keep ? part : -INFINITY;
+        if constexpr (kMaskAll) {
+          const int t = r0 + 16 * tile + 4 * c + i;
+          // t0 <= t < t_end, as one unsigned compare
+          bool keep = static_cast<uint32_t>(t - t0) < n_keep && col_used;
+          if constexpr (kQG) keep = keep && t <= col_hi && t >= col_lo;
+          sc[4 * u + i] = keep ? part : -INFINITY;
+        } else {
+          sc[4 * u + i] = part;
+        }
+      }
+      if constexpr (!kMaskAll) {
+        if (!full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = r0 + 16 * tile + 4 * c + i;
+            if (static_cast<uint32_t>(t - t0) >= n_keep) sc[4 * u + i] = -INFINITY;
+          }
+        }
       }
     };
     if constexpr (PACK) {
@@ -472,7 +509,10 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       const v4f vb = scale4(3, gn, PACK ? T : u);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float pj = sc[4 * u + i] == -INFINITY ? 0.0f : fast_exp2(sc[4 * u + i] - m_run);
+        // (a masked score gives 2^-inf = 0 as long as m_run is finite: with
+        // packed columns every column scores every key, and a processed
+        // iteration holds at least one key, so only the other forms test)
+        const float pj = (PACK && !kQG) || sc[4 * u + i] != -INFINITY ? fast_exp2(sc[4 * u + i] - m_run) : 0.0f;
         pw[4 * u + i] = pj;
         l_run += pj;
         bacc = fmaf(pj, vb[i], bacc);
@@ -492,23 +532,35 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       }
     }
     const v4f vs0 = scale4(2, gn, 0), vs1 = scale4(2, gn, 1);
-    __bf16 hi[8], lo[8];
+    // Weights in bf16 pairs (slots 2k, 2k + 1: one B operand word), hi part
+    // and lo = w - hi, each pair converted by one packed conversion; the
+    // weight sum of the 128 offset takes a word per v_dot2 with (1, 1).
+    uint32_t bh[4], bl[4];
+    const v2bf ones = __builtin_bit_cast(v2bf, 0x3F803F80u);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float w = ps[j] * (j < 4 ? vs0[j] : vs1[j - 4]);
-      hi[j] = static_cast<__bf16>(w);
-      const float hf = static_cast<float>(hi[j]);
-      lo[j] = static_cast<__bf16>(w - hf);
+    for (int k = 0; k < 4; ++k) {
+      const int j = 2 * k;
+      // (fma with + 0: the fp16 scale converts inside the multiply)
+      const float w0 = fmaf(ps[j], j < 4 ? vs0[j] : vs1[j - 4], 0.0f);
+      const float w1 = fmaf(ps[j + 1], j + 1 < 4 ? vs0[j + 1] : vs1[j - 3], 0.0f);
+      uint32_t hb = __builtin_bit_cast(uint32_t, v2bf{static_cast<__bf16>(w0), static_cast<__bf16>(w1)});
+      asm("" : "+v"(hb));  // h0, h1 from the packed word (no second conversion of w0)
+      const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xFFFF0000u);
+      const uint32_t lb =
+          __builtin_bit_cast(uint32_t, v2bf{static_cast<__bf16>(w0 - h0), static_cast<__bf16>(w1 - h1)});
       if constexpr (PACK) {
         // column n + 8T takes part T of the weight
-        hi[j] = T ? lo[j] : hi[j];
-        wsum += static_cast<float>(hi[j]);
+        bh[k] = T ? lb : hb;
+        wsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, bh[k]), ones, wsum, false);
       } else {
-        wsum += hf + static_cast<float>(lo[j]);
+        bh[k] = hb;
+        bl[k] = lb;
+        wsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, hb), ones, wsum, false);
+        wsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, lb), ones, wsum, false);
       }
     }
-    const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
-    const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+    const v8bf bhi = __builtin_bit_cast(v8bf, u32x4{bh[0], bh[1], bh[2], bh[3]});
+    const v8bf blo = __builtin_bit_cast(v8bf, u32x4{bl[0], bl[1], bl[2], bl[3]});
 
     // P . V on the bf16 matrix cores: A = (128 + nibble) of 16 dims x 32 keys
 #pragma unroll
@@ -542,7 +594,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   };
 
   auto load_next = [&](IterBuf<D, F32>& B, int t0) {
-    load_iter<D, G, F32, kStreamNT>(B, kq_row0, vq_row0, sc_arr, lr, min(t0, last), last, m, c, vhalf);
+    load_iter<D, G, F32, kStreamNT>(B, kq_row0, vq_row0, sc_arr, lo, block_row(t0));
   };
 
   auto pace = [&](int done) { pace_waves<NW>(s_done, wv, lane, done); };

@@ -109,7 +109,9 @@ int tq_sdpa_int4_noalloc(const void* q, tq_dtype q_dtype,
  * tq_sdpa_int4 (max_kv_len = kv_len), 1 = tq_sdpa_int4_ragged, 2 =
  * tq_sdpa_int4_prefill (batch = n_new, max_kv_len = n_prior + n_new).
  * *splits = workgroups per sequence along the keys (grid x), *chunk_keys =
- * keys per split; the kernel's name is written to kernel[kernel_bytes]. */
+ * keys per split; the kernel's name is written to kernel[kernel_bytes].
+ * The cache capacity is taken as max_kv_len: caches of fewer than 32 rows
+ * run the VALU kernel (the matrix-core kernel reads 32-row blocks). */
 int tq_sdpa_int4_plan(int mode, int batch, int num_heads, int num_kv_heads, int head_dim,
                       int max_kv_len, tq_dtype sb_dtype, int sliding_window, int* splits,
                       int* chunk_keys, char* kernel, size_t kernel_bytes);
