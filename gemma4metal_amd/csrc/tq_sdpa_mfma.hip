@@ -30,6 +30,8 @@
 // Scale/bias of 32 keys are staged through 1 KB of LDS per wave, transposed
 // to [array][group][key] so each lane reads its 8 values with two 8 B reads.
 // Loads are double-buffered one iteration (9 KB per wave) ahead.
+#include <type_traits>
+
 #include "tq_sdpa_common.h"
 
 namespace tq {
@@ -98,9 +100,10 @@ __device__ __forceinline__ T stream_load(const T* p) {
 // the block's base (scalar registers) plus a constant lane offset and an
 // immediate row offset, so an iteration spends no vector instructions on
 // addresses.  The caller keeps rows r0 .. r0 + 31 inside the cache
-// (block_row).
-template <int D, int G, bool F32, bool kNT>
-__device__ __forceinline__ void load_iter(IterBuf<D, F32>& B, const uint32_t* kq_row0,
+// (block_row).  In three parts, in the order the products consume them:
+// 0 = scales and K, 1 = V slots 0-3, 2 = V slots 4-7.
+template <int PART, int D, int G, bool F32, bool kNT>
+__device__ __forceinline__ void load_part(IterBuf<D, F32>& B, const uint32_t* kq_row0,
                                           const uint32_t* vq_row0, const uint32_t* sc_arr,
                                           const LaneOffs& lo, int r0) {
   using Gm = MGeom<D, G, F32>;
@@ -108,46 +111,59 @@ __device__ __forceinline__ void load_iter(IterBuf<D, F32>& B, const uint32_t* kq
   // (uniform base + zero-extended lane offset, then the constant row offset
   // as a separate addition: the form the compiler folds into the
   // instruction's scalar base, vector offset and immediate)
-  const char* kb = reinterpret_cast<const char*>(kq_row0 + static_cast<int64_t>(r0) * (D / 8)) + lo.k;
-  const char* vb = reinterpret_cast<const char*>(vq_row0 + static_cast<int64_t>(r0) * (D / 8)) + lo.v;
-  const char* sb = reinterpret_cast<const char*>(sc_arr + static_cast<int64_t>(r0) * Gm::SCW) + lo.s;
+  if constexpr (PART == 0) {
+    const char* sb = reinterpret_cast<const char*>(sc_arr + static_cast<int64_t>(r0) * Gm::SCW) + lo.s;
 #pragma unroll
-  for (int tile = 0; tile < 2; ++tile) {
+    for (int e = 0; e < 2; ++e) {
+      const char* a = sb + e * (Gm::SCW * 4);
+      if constexpr (Gm::SCW >= 4) {
 #pragma unroll
-    for (int w = 0; w < Gm::KW; w += 4) {
-      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(kb + (tile * 16 * RB + w * 4)));
-      B.kw[tile][w] = u.x; B.kw[tile][w + 1] = u.y; B.kw[tile][w + 2] = u.z; B.kw[tile][w + 3] = u.w;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const char* a = vb + (16 * (j >> 2) + (j & 3)) * RB;
-    if constexpr (Gm::VWH == 4) {
-      const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(a));
-      B.vw[j][0] = u.x; B.vw[j][1] = u.y; B.vw[j][2] = u.z; B.vw[j][3] = u.w;
-    } else if constexpr (Gm::VWH == 2) {
-      const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(a));
-      B.vw[j][0] = u.x; B.vw[j][1] = u.y;
-    } else {
-      B.vw[j][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(a));
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const char* a = sb + e * (Gm::SCW * 4);
-    if constexpr (Gm::SCW >= 4) {
-#pragma unroll
-      for (int w = 0; w < Gm::SCW; w += 4) {
-        const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(a + 4 * w));
-        B.sc[e][w] = u.x; B.sc[e][w + 1] = u.y; B.sc[e][w + 2] = u.z; B.sc[e][w + 3] = u.w;
+        for (int w = 0; w < Gm::SCW; w += 4) {
+          const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(a + 4 * w));
+          B.sc[e][w] = u.x; B.sc[e][w + 1] = u.y; B.sc[e][w + 2] = u.z; B.sc[e][w + 3] = u.w;
+        }
+      } else if constexpr (Gm::SCW == 2) {
+        const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(a));
+        B.sc[e][0] = u.x; B.sc[e][1] = u.y;
+      } else {
+        B.sc[e][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(a));
       }
-    } else if constexpr (Gm::SCW == 2) {
-      const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(a));
-      B.sc[e][0] = u.x; B.sc[e][1] = u.y;
-    } else {
-      B.sc[e][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(a));
+    }
+    const char* kb = reinterpret_cast<const char*>(kq_row0 + static_cast<int64_t>(r0) * (D / 8)) + lo.k;
+#pragma unroll
+    for (int tile = 0; tile < 2; ++tile) {
+#pragma unroll
+      for (int w = 0; w < Gm::KW; w += 4) {
+        const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(kb + (tile * 16 * RB + w * 4)));
+        B.kw[tile][w] = u.x; B.kw[tile][w + 1] = u.y; B.kw[tile][w + 2] = u.z; B.kw[tile][w + 3] = u.w;
+      }
+    }
+  } else {
+    const char* vb = reinterpret_cast<const char*>(vq_row0 + static_cast<int64_t>(r0) * (D / 8)) + lo.v;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = 4 * (PART - 1) + jj;
+      const char* a = vb + (16 * (j >> 2) + (j & 3)) * RB;
+      if constexpr (Gm::VWH == 4) {
+        const u32x4 u = stream_load<kNT>(reinterpret_cast<const u32x4*>(a));
+        B.vw[j][0] = u.x; B.vw[j][1] = u.y; B.vw[j][2] = u.z; B.vw[j][3] = u.w;
+      } else if constexpr (Gm::VWH == 2) {
+        const u32x2 u = stream_load<kNT>(reinterpret_cast<const u32x2*>(a));
+        B.vw[j][0] = u.x; B.vw[j][1] = u.y;
+      } else {
+        B.vw[j][0] = stream_load<kNT>(reinterpret_cast<const uint32_t*>(a));
+      }
     }
   }
+}
+
+template <int D, int G, bool F32, bool kNT>
+__device__ __forceinline__ void load_iter(IterBuf<D, F32>& B, const uint32_t* kq_row0,
+                                          const uint32_t* vq_row0, const uint32_t* sc_arr,
+                                          const LaneOffs& lo, int r0) {
+  load_part<0, D, G, F32, kNT>(B, kq_row0, vq_row0, sc_arr, lo, r0);
+  load_part<1, D, G, F32, kNT>(B, kq_row0, vq_row0, sc_arr, lo, r0);
+  load_part<2, D, G, F32, kNT>(B, kq_row0, vq_row0, sc_arr, lo, r0);
 }
 
 __device__ __forceinline__ float half_lo(uint32_t w) {
@@ -384,10 +400,17 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     }
   };
 
-  auto process = [&](const IterBuf<D, F32>& B, int t0) {
+  // `issue(part)` puts out part 0, 1, 2 of the next block's loads at three
+  // points of the products (before the scale staging, after the K MFMAs,
+  // before the V products): a wave's loads go out in three smaller bursts,
+  // so the waves of a CU stay closer together than with one burst of all
+  // thirteen loads per iteration.
+  auto process = [&](const IterBuf<D, F32>& B, int t0, auto&& issue) {
     // B holds the block of rows r0 .. r0 + 31 (r0 <= t0); its keys below t0
     // or from t_end on are masked
     const int r0 = block_row(t0);
+    issue(std::integral_constant<int, 0>{});
+    __builtin_amdgcn_sched_barrier(0);
     const uint32_t n_keep = static_cast<uint32_t>(t_end - t0);  // > 0 for a processed iteration
     // scales -> LDS [array][group][key]
 #pragma unroll
@@ -470,6 +493,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
       for (int k = 0; k < 3; ++k) acc[k] = v4i{0, 0, 0, 0};
       kq_tile(0, acc, 0);
       kq_tile(1, acc, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(std::integral_constant<int, 1>{});
+      __builtin_amdgcn_sched_barrier(0);
       scores(acc, 0, T);
     } else {
 #pragma unroll
@@ -478,6 +504,11 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 #pragma unroll
         for (int k = 0; k < 3; ++k) acc[k] = v4i{0, 0, 0, 0};
         kq_tile(tile, acc, 0);
+        if (tile == 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue(std::integral_constant<int, 1>{});
+          __builtin_amdgcn_sched_barrier(0);
+        }
         scores(acc, tile, tile);
       }
     }
@@ -562,6 +593,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     const v8bf bhi = __builtin_bit_cast(v8bf, u32x4{bh[0], bh[1], bh[2], bh[3]});
     const v8bf blo = __builtin_bit_cast(v8bf, u32x4{bl[0], bl[1], bl[2], bl[3]});
 
+    __builtin_amdgcn_sched_barrier(0);
+    issue(std::integral_constant<int, 2>{});
+    __builtin_amdgcn_sched_barrier(0);
     // P . V on the bf16 matrix cores: A = (128 + nibble) of 16 dims x 32 keys
 #pragma unroll
     for (int s = 0; s < VWH; ++s) {
@@ -593,9 +627,14 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     }
   };
 
-  auto load_next = [&](IterBuf<D, F32>& B, int t0) {
-    load_iter<D, G, F32, kStreamNT>(B, kq_row0, vq_row0, sc_arr, lo, block_row(t0));
+  // the next block's loads (into B, rows from key t0), issued in parts by process
+  auto next_of = [&](IterBuf<D, F32>& B, int t0) {
+    const int r0 = block_row(t0);
+    return [&B, r0, &kq_row0, &vq_row0, &sc_arr, &lo](auto part) {
+      load_part<decltype(part)::value, D, G, F32, kStreamNT>(B, kq_row0, vq_row0, sc_arr, lo, r0);
+    };
   };
+  auto no_loads = [](auto) {};
 
   auto pace = [&](int done) { pace_waves<NW>(s_done, wv, lane, done); };
   pace(0);
@@ -605,25 +644,19 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // before their reuse after the loop, a full memory round trip per wave.
   int it = 0;
   for (; it + 2 < nit; it += 2) {
-    load_next(bufB, base0 + (it + 1) * kIter);
-    __builtin_amdgcn_sched_barrier(0);
-    process(bufA, base0 + it * kIter);
+    process(bufA, base0 + it * kIter, next_of(bufB, base0 + (it + 1) * kIter));
     pace(it + 1);
     __builtin_amdgcn_sched_barrier(0);
-    load_next(bufA, base0 + (it + 2) * kIter);
-    __builtin_amdgcn_sched_barrier(0);
-    process(bufB, base0 + (it + 1) * kIter);
+    process(bufB, base0 + (it + 1) * kIter, next_of(bufA, base0 + (it + 2) * kIter));
     pace(it + 2);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (it + 1 < nit) {
-    load_next(bufB, base0 + (it + 1) * kIter);
+    process(bufA, base0 + it * kIter, next_of(bufB, base0 + (it + 1) * kIter));
     __builtin_amdgcn_sched_barrier(0);
-    process(bufA, base0 + it * kIter);
-    __builtin_amdgcn_sched_barrier(0);
-    process(bufB, base0 + (it + 1) * kIter);
+    process(bufB, base0 + (it + 1) * kIter, no_loads);
   } else if (it < nit) {
-    process(bufA, base0 + it * kIter);
+    process(bufA, base0 + it * kIter, no_loads);
   }
 
   // ---- per-wave result into the finalisation arena --------------------------
