@@ -45,8 +45,8 @@ def measured_traffic():
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--sets", type=int, default=8, help="distinct KV sets rotated")
     ap.add_argument("--workload", default="ctx32k",
                     choices=["ctx32k", "sweep", "sliding50", "ragged", "stream", "polar", "global",
