@@ -46,6 +46,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 constexpr int kHcWaves = 4;
 constexpr int kHcD = 512;
@@ -756,11 +757,17 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
 #pragma unroll
       for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i)
           sc[tile][i] = sf * (sc[tile][i] + __int_as_float(__builtin_amdgcn_mov_dpp(
                                                  __float_as_int(sc[tile][i]), 0x128, 0xF, 0xF, false)));
-          if (t0 + 16 * tile + 4 * c + i >= t_end) sc[tile][i] = -INFINITY;
-        }
+      // keys from t_end on: only the last step of a stream reaches them
+      if (t0 + 32 > t_end) {  // uniform
+#pragma unroll
+        for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (t0 + 16 * tile + 4 * c + i >= t_end) sc[tile][i] = -INFINITY;
+      }
 
       // online softmax (lazy rescale); the factor goes to the consumer
       float mt = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
@@ -782,6 +789,9 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
         m_run = m_new;
       }
       if (c == 0) f_lds[slot][s][m] = f;
+      // (every stream runs the steps of the longest one, so a stream's steps
+      // can all lie past t_end: m_run is then -inf, and masked scores need
+      // the explicit 0)
       float pw[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -797,21 +807,32 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
         // slot j: key 16 (j / 4) + 4c + j % 4
         const v4f vs[2] = {scale4(2, gv, 4 * c), scale4(2, gv, 16 + 4 * c)};
         const v4f vb[2] = {scale4(3, gv, 4 * c), scale4(3, gv, 16 + 4 * c)};
-        __bf16 hi[8], lo[8];
+        // weights in bf16 pairs (slots 2k, 2k + 1: one B operand word): hi
+        // and lo = w - hi, each pair by one packed conversion; the weight
+        // sum of the 128 offset takes a word per v_dot2 with (1, 1); the
+        // fp16 scales convert inside the multiplies (fma with + 0)
+        uint32_t bh[4], bl[4];
+        const v2bf ones = __builtin_bit_cast(v2bf, 0x3F803F80u);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float w = pw[j] * vs[j >> 2][j & 3];
-          hi[j] = static_cast<__bf16>(w);
-          const float hf = static_cast<float>(hi[j]);
-          lo[j] = static_cast<__bf16>(w - hf);
-          wsum[blk] += hf + static_cast<float>(lo[j]);
+        for (int k = 0; k < 4; ++k) {
+          const int j = 2 * k;
+          const float w0 = fmaf(pw[j], vs[j >> 2][j & 3], 0.0f);
+          const float w1 = fmaf(pw[j + 1], vs[(j + 1) >> 2][(j + 1) & 3], 0.0f);
+          uint32_t hb = __builtin_bit_cast(uint32_t, v2bf{static_cast<__bf16>(w0), static_cast<__bf16>(w1)});
+          asm("" : "+v"(hb));  // h0, h1 from the packed word
+          const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xFFFF0000u);
+          const uint32_t lb =
+              __builtin_bit_cast(uint32_t, v2bf{static_cast<__bf16>(w0 - h0), static_cast<__bf16>(w1 - h1)});
+          bh[k] = hb;
+          bl[k] = lb;
+          wsum[blk] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, hb), ones, wsum[blk], false);
+          wsum[blk] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, lb), ones, wsum[blk], false);
           bacc[blk] = fmaf(pw[j], vb[j >> 2][j & 3], bacc[blk]);
+          bacc[blk] = fmaf(pw[j + 1], vb[(j + 1) >> 2][(j + 1) & 3], bacc[blk]);
         }
-        const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
-        const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
         uint4* dst = pv_lds + (((slot * NS + s) * 4 + blk) * 2) * 64 + lane;
-        dst[0] = __builtin_bit_cast(uint4, bhi);
-        dst[64] = __builtin_bit_cast(uint4, blo);
+        dst[0] = uint4{bh[0], bh[1], bh[2], bh[3]};
+        dst[64] = uint4{bl[0], bl[1], bl[2], bl[3]};
       }
     };
 
