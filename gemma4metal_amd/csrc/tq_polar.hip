@@ -1112,6 +1112,7 @@ __device__ __forceinline__ float2 sb_pair<float>(const uint32_t* w) {
 }
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
@@ -1270,18 +1271,28 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
       const float pj[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
       const float sj[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
       const float bj[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
-      __bf16 hi[8], lo[8];
+      // weights in bf16 pairs (slots 2k, 2k + 1: one B operand word): hi and
+      // lo = w - hi, each pair by one packed conversion; the weight sum of
+      // the 128 offset takes a word per v_dot2 with (1, 1)
+      uint32_t bh[4], bl[4];
+      const v2bf ones = __builtin_bit_cast(v2bf, 0x3F803F80u);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float w = pj[j] * sj[j];
-        hi[j] = static_cast<__bf16>(w);
-        const float hf = static_cast<float>(hi[j]);
-        lo[j] = static_cast<__bf16>(w - hf);
-        wsum += hf + static_cast<float>(lo[j]);
-        bacc = fmaf(pj[j], bj[j], bacc);
+      for (int k = 0; k < 4; ++k) {
+        const float w0 = pj[2 * k] * sj[2 * k], w1 = pj[2 * k + 1] * sj[2 * k + 1];
+        uint32_t hb = __builtin_bit_cast(uint32_t, v2bf{static_cast<__bf16>(w0), static_cast<__bf16>(w1)});
+        asm("" : "+v"(hb));  // h0, h1 from the packed word
+        const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xFFFF0000u);
+        const uint32_t lb =
+            __builtin_bit_cast(uint32_t, v2bf{static_cast<__bf16>(w0 - h0), static_cast<__bf16>(w1 - h1)});
+        bh[k] = hb;
+        bl[k] = lb;
+        wsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, hb), ones, wsum, false);
+        wsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf, lb), ones, wsum, false);
+        bacc = fmaf(pj[2 * k], bj[2 * k], bacc);
+        bacc = fmaf(pj[2 * k + 1], bj[2 * k + 1], bacc);
       }
-      const v8bf bhi = v8bf{hi[0], hi[1], hi[2], hi[3], hi[4], hi[5], hi[6], hi[7]};
-      const v8bf blo = v8bf{lo[0], lo[1], lo[2], lo[3], lo[4], lo[5], lo[6], lo[7]};
+      const v8bf bhi = __builtin_bit_cast(v8bf, u32x4v{bh[0], bh[1], bh[2], bh[3]});
+      const v8bf blo = __builtin_bit_cast(v8bf, u32x4v{bl[0], bl[1], bl[2], bl[3]});
 #pragma unroll
       for (int by = 0; by < 4; ++by) {
         // byte `by` of the words of slots 2r, 2r+1 -> the two 16-bit halves

@@ -740,7 +740,10 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
           const v4f ks = scale4(0, gl, 16 * tile + 4 * c), kb = scale4(1, gl, 16 * tile + 4 * c);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float dot = static_cast<float>((acc2[i] << 16) + ((acc1[i] << 8) + acc0[i]));
+            // two shift-adds (the compiler's add3 form takes three instructions)
+            int lo01 = (acc1[i] << 8) + acc0[i];
+            asm("" : "+v"(lo01));
+            const float dot = static_cast<float>((acc2[i] << 16) + lo01);
             sc[tile][i] = fmaf(dot, ks[i], fmaf(kb[i], qh[P], sc[tile][i]));
           }
         }
