@@ -671,6 +671,11 @@ constexpr int kP7QTab = 1024 + 4096 + 16;
 
 struct P7Keys {
   const float* qtab;      // [Hq][kP7QTab]
+  // attention straight from q (build_p7_tables): q [Hq][128], P [128][128]
+  // (null: q' = q) and S P [128][128]; null otherwise
+  const float* q;
+  const float* P;
+  const float* SP;
   const float* cs;        // cs1[16][2] then cs2[4][2]
   const uint32_t* angles; // [Hkv][cap][12]
   const uint32_t* norms;  // [Hkv][cap]
@@ -736,6 +741,100 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
     const float cp = c2[2 * kp], sp = c2[2 * kp + 1];
     T.t2[threadIdx.x] = make_float4(cp * c2[2 * k0], cp * c2[2 * k0 + 1], sp * c2[2 * k1],
                                     sp * c2[2 * k1 + 1]);
+  }
+  __syncthreads();
+}
+
+// The tables of load_p7_tables built in the workgroup from q, P and S P
+// (the work of polar7_prepare_sp_kernel, for the G heads of this workgroup
+// only): q' = P q (q' = q without P) and u = S q' = (S P) q, then t1, tq, U
+// and t2.  Every wave takes 32 of the 256 rows of [P; S P] in four passes
+// of 8 rows: lane (row 8 r + l / 8, j = l % 8) loads float4 columns 8c + j,
+// c = 0..3, so each load instruction reads 8 whole 128-byte lines, and the
+// 8 lanes of a row finish its dot products with a DPP butterfly.  All NT
+// threads call it; it ends with a barrier.
+template <int G, int NT>
+__device__ __forceinline__ void build_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0) {
+  static_assert(NT == 512, "eight waves of 32 rows cover [P; S P]");
+  __shared__ __attribute__((aligned(16))) float xs[G][128];
+  __shared__ float qp[G][128], us[G][128], csl[40];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int j = lane & 7, rs = lane >> 3;
+  // rows of this wave: P rows 32 w .. (w < 4), S P rows 32 (w - 4) .. (w >=
+  // 4); without P the first four waves read S P as well and drop the sums
+  const bool is_p = wave < 4;
+  const float* mat = (is_p && k.P) ? k.P : k.SP;
+  const int row0 = 32 * (wave & 3);
+  float4 a[4][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      a[r][c] = *reinterpret_cast<const float4*>(mat + (row0 + 8 * r + rs) * 128 + 4 * (8 * c + j));
+  if (t < G * 128) xs[t >> 7][t & 127] = k.q[static_cast<int64_t>(h0) * 128 + t];
+  if (t < 40) csl[t] = k.cs[t];
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float4 x[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const float4*>(&xs[g][4 * (8 * c + j)]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        acc = fmaf(a[r][c].x, x[c].x, acc);
+        acc = fmaf(a[r][c].y, x[c].y, acc);
+        acc = fmaf(a[r][c].z, x[c].z, acc);
+        acc = fmaf(a[r][c].w, x[c].w, acc);
+      }
+      acc = group_sum<8>(acc);
+      const int row = row0 + 8 * r + rs;
+      if (j == 0) {
+        if (!is_p) us[g][row] = acc;
+        else qp[g][row] = k.P ? acc : xs[g][row];
+      }
+    }
+  }
+  __syncthreads();
+  // level-1 table t1[row(jj)][c][g] = q'[2 jj] cos c + q'[2 jj + 1] sin c
+  for (int e = t; e < 64 * 16 * G; e += NT) {
+    const int g = e % G, c = (e / G) & 15, jj = e / (16 * G);
+    T.t1[p7_t1_row(jj)][c][g] = qp[g][2 * jj] * csl[2 * c] + qp[g][2 * jj + 1] * csl[2 * c + 1];
+  }
+  // QJL byte table tq[pos][16 hi + lo][g]: the set bits of lo over u rows
+  // 8 pos .. + 3, of hi over rows 8 pos + 4 .. + 7
+  for (int e = t; e < 16 * 16 * G; e += NT) {
+    const int g = e % G, lo = (e / G) & 15, pos = e / (16 * G);
+    const float* uu = &us[g][8 * pos];
+    float slo = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) slo += ((lo >> i) & 1) ? uu[i] : 0.0f;
+    const float u4 = uu[4], u5 = uu[5], u6 = uu[6], u7 = uu[7];
+#pragma unroll
+    for (int hi = 0; hi < 16; ++hi) {
+      float sum = slo;
+      if (hi & 1) sum += u4;
+      if (hi & 2) sum += u5;
+      if (hi & 4) sum += u6;
+      if (hi & 8) sum += u7;
+      T.tq[pos][16 * hi + lo][g] = sum;
+    }
+  }
+  if (t < 64) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sum = wave_sum_f(us[g][t] + us[g][t + 64]);
+      if (t == 0) T.U[g] = sum;
+    }
+  }
+  if (t >= 64 && t < 128) {
+    const int i = t - 64;
+    const int kp = i & 3, k0 = (i >> 2) & 3, k1 = i >> 4;
+    const float* c2 = csl + 32;
+    const float cp = c2[2 * kp], sp = c2[2 * kp + 1];
+    T.t2[i] = make_float4(cp * c2[2 * k0], cp * c2[2 * k0 + 1], sp * c2[2 * k1], sp * c2[2 * k1 + 1]);
   }
   __syncthreads();
 }
@@ -1137,7 +1236,9 @@ __device__ __forceinline__ int p7_slot(int t) { return (t & 32) | ((t & 3) << 3)
 // per CU, sharing the workgroup's staged query tables.
 constexpr int kP7Waves = 8;
 
-template <int G, typename SB, int NW>
+// FUSED: the query tables are built in the prologue from q, P and S P
+// (build_p7_tables) instead of read from k.qtab.
+template <int G, typename SB, int NW, bool FUSED = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void polar7_sdpa_kernel(SdpaParams p, P7Keys k) {
   pin_args(p);
   asm volatile("" ::"s"(k.qtab), "s"(k.cs), "s"(k.angles), "s"(k.norms), "s"(k.qjl));
@@ -1176,7 +1277,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
     for (int u = 0; u < 4; ++u) load_sub(key[u], base0, u);
   }
-  load_p7_tables<G, NW * 64>(T, k, h0);
+  if constexpr (FUSED)
+    build_p7_tables<G, NW * 64>(T, k, h0);
+  else
+    load_p7_tables<G, NW * 64>(T, k, h0);
 
   float m_run[G], l_run[G];
 #pragma unroll
@@ -1874,6 +1978,47 @@ int tq_polar7_sdpa_int4v(const float* q_tables, const uint32_t* angles,
     else polar7_sdpa_kernel<2, float, NW><<<grid, NT, 0, s>>>(p, k);
   }
   TQ_CHECK_LAUNCH("polar7_sdpa_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_sdpa_int4v_q(const float* q, const float* precondition,
+                           const float* sketch_precondition, const float* cs_tables,
+                           const uint32_t* angles, const uint32_t* norms, const uint32_t* qjl,
+                           const uint32_t* v_quant, const void* v_scales, const void* v_biases,
+                           tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
+                           int kv_len, int kv_capacity, float scale, int sliding_window,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "tq_polar7_sdpa_int4v_q";
+  TQ_CHECK_ARG(q && sketch_precondition && cs_tables && angles && norms && qjl, "%s: null pointer", fn);
+  TQ_CHECK_ARG(num_kv_heads >= 1 && num_heads >= num_kv_heads && num_heads % num_kv_heads == 0,
+               "%s: num_heads must be a multiple of num_kv_heads", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(angles) % 16 == 0 && reinterpret_cast<uintptr_t>(qjl) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(sketch_precondition) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(precondition) % 16 == 0,
+               "%s: angles / qjl / precondition / sketch_precondition must be 16-byte aligned", fn);
+  TQ_CHECK_ARG(v_quant && v_scales && v_biases, "%s: null V pointer", fn);
+  TQ_CHECK_ARG(sb_dtype == TQ_F16 || sb_dtype == TQ_F32, "%s: sb_dtype must be f16 or f32", fn);
+  P7Keys k{};
+  k.cs = cs_tables;
+  k.angles = angles; k.norms = norms; k.qjl = qjl;
+  k.q = q; k.P = precondition; k.SP = sketch_precondition;
+  SdpaParams p;
+  dim3 grid;
+  int G = 1;
+  int st = polar_sdpa_params(p, num_heads, num_kv_heads, 128, kv_len, kv_capacity, scale, sliding_window,
+                             0.0f, kP7MaxG, out, workspace, workspace_bytes, grid, G, fn);
+  if (st != TQ_OK) return st;
+  p.vq = v_quant; p.vs = v_scales; p.vb = v_biases;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  constexpr int NW = kP7Waves, NT = kP7Waves * 64;
+  if (sb_dtype == TQ_F16) {
+    if (G == 1) polar7_sdpa_kernel<1, __half, NW, true><<<grid, NT, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<2, __half, NW, true><<<grid, NT, 0, s>>>(p, k);
+  } else {
+    if (G == 1) polar7_sdpa_kernel<1, float, NW, true><<<grid, NT, 0, s>>>(p, k);
+    else polar7_sdpa_kernel<2, float, NW, true><<<grid, NT, 0, s>>>(p, k);
+  }
+  TQ_CHECK_LAUNCH("polar7_sdpa_kernel (fused query tables)");
   return TQ_OK;
 }
 

@@ -351,3 +351,30 @@ class Polar7Codec:
              _ptr(self.cs), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases), sbt, _ptr(out), Hq, Hkv,
              n, cap, float(scale), int(sliding_window), _ptr(ws), ws.numel(), sh)
         return out
+
+    def sdpa_int4v_q(self, q: torch.Tensor, angles, norms, qjl, v_quant, v_scales, v_biases,
+                     scale: float = 1.0, sliding_window: int = 0, *, kv_len: Optional[int] = None,
+                     out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """``sdpa_int4v`` straight from the query q (Hq, 128) f32: every
+        workgroup builds its heads' query tables itself, so a decode step is
+        one launch (no ``prepare_query``).  Returns (Hq, 128) f32."""
+        _check_cuda("q", q)
+        _need(q.dim() == 2 and q.shape[1] == P7_D and q.dtype == torch.float32 and q.is_contiguous(),
+              "q must be contiguous (Hq, 128) f32")
+        Hq = q.shape[0]
+        Hkv, cap = angles.shape[0], angles.shape[1]
+        _check_cuda("v_quant", v_quant)
+        _need(v_quant.shape == (Hkv, cap, P7_D // 8), "v_quant must be (Hkv, cap, 16)")
+        _need(v_scales.dtype in (torch.float16, torch.float32), "v_scales must be f16 or f32")
+        sbt = TQ_F16 if v_scales.dtype == torch.float16 else TQ_F32
+        n = cap if kv_len is None else int(kv_len)
+        if out is None:
+            out = torch.empty((Hq, P7_D), dtype=torch.float32, device=q.device)
+        nbytes = _lib.load().tq_polar7_sdpa_workspace_size(Hq, Hkv, n)
+        sh = _stream(stream)
+        ws = workspace(nbytes, q.device, sh)
+        call("tq_polar7_sdpa_int4v_q", _ptr(q), _ptr(self.P), _ptr(self.SP), _ptr(self.cs),
+             _ptr(angles), _ptr(norms), _ptr(qjl), _ptr(v_quant), _ptr(v_scales), _ptr(v_biases),
+             sbt, _ptr(out), Hq, Hkv, n, cap, float(scale), int(sliding_window), _ptr(ws),
+             ws.numel(), sh)
+        return out

@@ -373,6 +373,18 @@ int tq_polar7_sdpa_int4v(const float* q_tables, const uint32_t* angles,
                          tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
                          int kv_len, int kv_capacity, float scale, int sliding_window,
                          void* workspace, size_t workspace_bytes, void* stream);
+/* The same attention straight from q [num_heads, 128] f32: each workgroup
+ * builds the query tables of its heads (as tq_polar7_prepare_query_sp, from
+ * precondition P -- NULL: q' = q -- and sketch_precondition = S P) in its
+ * prologue, so a decode step is one launch.  No counterpart in the
+ * reference (polar7 and QJL are this build's, README.md:11,176). */
+int tq_polar7_sdpa_int4v_q(const float* q, const float* precondition,
+                           const float* sketch_precondition, const float* cs_tables,
+                           const uint32_t* angles, const uint32_t* norms, const uint32_t* qjl,
+                           const uint32_t* v_quant, const void* v_scales, const void* v_biases,
+                           tq_dtype sb_dtype, float* out, int num_heads, int num_kv_heads,
+                           int kv_len, int kv_capacity, float scale, int sliding_window,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -281,6 +281,41 @@ def test_polar7_sdpa_int4v(pq, Hq, Hkv, L, W, sb):
     assert_close(got, ref, f"polar7 sdpa Hq{Hq} Hkv{Hkv} L{L} W{W} {sb}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,L,W,sb,rot", [
+    (32, 16, 3000, 0, "f16", True), (32, 16, 3000, 1024, "f16", True), (4, 4, 1, 0, "f32", True),
+    (8, 1, 5000, 0, "f16", False), (16, 2, 20000, 0, "f32", True), (2, 2, 400, 0, "f16", False)])
+def test_polar7_sdpa_int4v_q(pq, Hq, Hkv, L, W, sb, rot):
+    """Attention straight from q (query tables built in each workgroup):
+    against the oracle, and against the two-launch path on the same
+    inputs (same tables up to the order of the fp32 sums of q' and S q':
+    the scores then differ in the last bits, and so may the bf16 hi/lo split
+    of a weight, ~2^-17 of it)."""
+    rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 5 * Hq + L + W, Hkv, L, rot=rot)
+    vq, vs, vb = O.quantize_int4(v, sb)
+    q = rng.standard_normal((Hq, 128)).astype(f32)
+    d = [dev(vq), dev(vs), dev(vb)]
+    got = host(codec.sdpa_int4v_q(dev(q), *dk, *d, 1.0, W))
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    two = host(codec.sdpa_int4v(tab, *dk, *d, 1.0, W))
+    assert np.max(np.abs(got - two)) < 1e-4, f"fused vs two-launch {np.max(np.abs(got - two)):.3e}"
+    ref = PQ.polar7_sdpa_int4v(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], vq, vs, vb,
+                               Hq // Hkv, 1.0, W)
+    assert_close(got, ref, f"polar7 fused sdpa Hq{Hq} Hkv{Hkv} L{L} W{W} {sb} rot{rot}")
+
+
+def test_polar7_sdpa_int4v_q_empty_and_prefix(pq):
+    rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 78, 2, 300)
+    vq, vs, vb = O.quantize_int4(v)
+    q = rng.standard_normal((4, 128)).astype(f32)
+    d = [dev(vq), dev(vs), dev(vb)]
+    assert not host(codec.sdpa_int4v_q(dev(q), *dk, *d, kv_len=0)).any()
+    got = host(codec.sdpa_int4v_q(dev(q), *dk, *d, kv_len=123))
+    _, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    ref = PQ.polar7_sdpa_int4v(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], vq, vs, vb, 2,
+                               kv_len=123)
+    assert_close(got, ref, "fused prefix 123")
+
+
 def test_polar7_sdpa_empty_and_prefix(pq):
     rng, codec, P, S, dk, hk, v = p7_cache_on_gpu(pq, 77, 2, 300)
     vq, vs, vb = O.quantize_int4(v)
@@ -304,12 +339,15 @@ def test_polar7_full_size_two_heads(pq):
     q = rng.standard_normal((Hq, 128)).astype(f32)
     tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
     got = host(codec.sdpa_int4v(tab, *dk, dev(vq), dev(vs), dev(vb)))
+    fused = host(codec.sdpa_int4v_q(dev(q), *dk, dev(vq), dev(vs), dev(vb)))
+    assert np.max(np.abs(fused - got)) < 1e-4, f"fused vs two-launch {np.max(np.abs(fused - got)):.3e}"
     hqp, hqs = host(qp), host(qs)
     for kvh in (0, 11):
         sl = slice(kvh, kvh + 1)
         ref = PQ.polar7_sdpa_int4v(hqp[2 * kvh:2 * kvh + 2], hqs[2 * kvh:2 * kvh + 2], hk[0][sl],
                                    host_norms(hk[1][sl]), hk[2][sl], vq[sl], vs[sl], vb[sl], 2)
         assert_close(got[2 * kvh:2 * kvh + 2], ref, f"kv head {kvh}")
+        assert_close(fused[2 * kvh:2 * kvh + 2], ref, f"fused, kv head {kvh}")
 
 
 def test_polar7_score_full_size_two_heads(pq):
