@@ -988,9 +988,13 @@ void sdpa_int4_hc2_kernel(SdpaParams p) {
         dst[0] = r[0]; dst[1] = r[1]; dst[2] = r[2]; dst[3] = r[3];
       }
     } else {
+      // read once, by the merge kernel: streaming (non-temporal) stores
       const int64_t slot = row * p.max_splits + split;
-      *reinterpret_cast<v4f*>(p.ws_o + slot * D + 4 * d4) = O;
-      if (d4 == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
+      __builtin_nontemporal_store(O, reinterpret_cast<v4f*>(p.ws_o + slot * D + 4 * d4));
+      if (d4 == 0) {
+        __builtin_nontemporal_store(M, p.ws_ml + slot * 2);
+        __builtin_nontemporal_store(L, p.ws_ml + slot * 2 + 1);
+      }
     }
   }
 }
