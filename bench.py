@@ -496,10 +496,15 @@ def bench_polar(args, torch, gen):
         s = i % nsets
         codec.score(prepared[s], *sets[s][0])
 
+    def score_q(i):
+        s = i % nsets
+        codec.score_q(qs_[s], *sets[s][0])
+
     ms_step, _, _ = time_launches(torch, step, args.steps, args.warmup)
     ms_two, _, _ = time_launches(torch, two_launch, args.steps, args.warmup)
     ms_attn, _, _ = time_launches(torch, attn_only, args.steps, args.warmup)
     ms_score, _, _ = time_launches(torch, score_only, args.steps, args.warmup)
+    ms_score_q, _, _ = time_launches(torch, score_q, args.steps, args.warmup)
     score_bytes = Hkv * L * 68 + 2 * Hq * D * 4 + Hq * L * 4
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     gbs_attn = nbytes / (ms_attn * 1e-3) / 1e9
@@ -523,7 +528,8 @@ def bench_polar(args, torch, gen):
                          "attention_us_per_launch": round(ms_attn * 1e3, 2),
                          "attention_gbs": round(gbs_attn, 1)},
           "score_only": {"us_per_launch": round(ms_score * 1e3, 2), "bytes_per_launch": score_bytes,
-                         "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1)}}, args)
+                         "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
+                         "from_q_us_per_launch": round(ms_score_q * 1e3, 2)}}, args)
 
 
 def emit(line, args):

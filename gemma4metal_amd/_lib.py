@@ -67,6 +67,7 @@ SIGNATURES = {
     "tq_polar7_sketch_precondition": (I, [P, P, P, P]),
     "tq_polar7_prepare_query_sp": (I, [P, P, P, P, I, P, P, P, P]),
     "tq_polar7_score": (I, [P, P, P, P, P, I, I, I, I, F, P, P]),
+    "tq_polar7_score_q": (I, [P, P, P, P, P, P, P, I, I, I, I, F, P, P]),
     "tq_polar7_sdpa_workspace_size": (SZ, [I, I, I]),
     "tq_polar7_sdpa_int4v": (I, [P, P, P, P, P, P, P, P, I, P, I, I, I, I, F, I, P, SZ, P]),
     "tq_polar7_sdpa_int4v_q": (I, [P, P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, F, I, P, SZ, P]),

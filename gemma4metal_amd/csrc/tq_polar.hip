@@ -748,26 +748,27 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
 // The tables of load_p7_tables built in the workgroup from q, P and S P
 // (the work of polar7_prepare_sp_kernel, for the G heads of this workgroup
 // only): q' = P q (q' = q without P) and u = S q' = (S P) q, then t1, tq, U
-// and t2.  Every wave takes 32 of the 256 rows of [P; S P] in four passes
-// of 8 rows: lane (row 8 r + l / 8, j = l % 8) loads float4 columns 8c + j,
-// c = 0..3, so each load instruction reads 8 whole 128-byte lines, and the
-// 8 lanes of a row finish its dot products with a DPP butterfly.  All NT
-// threads call it; it ends with a barrier.
+// and t2.  Every wave takes 256 / (NT / 64) of the 256 rows of [P; S P] in
+// passes of 8 rows: lane (row 8 r + l / 8, j = l % 8) loads float4 columns
+// 8c + j, c = 0..3, so each load instruction reads 8 whole 128-byte lines,
+// and the 8 lanes of a row finish its dot products with a DPP butterfly.
+// All NT threads call it; it ends with a barrier.
 template <int G, int NT>
 __device__ __forceinline__ void build_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0) {
-  static_assert(NT == 512, "eight waves of 32 rows cover [P; S P]");
+  static_assert(NT == 512 || NT == 1024, "8 or 16 waves cover the rows of [P; S P]");
+  constexpr int RPW = 256 / (NT / 64), NPS = RPW / 8;  // rows per wave, passes
   __shared__ __attribute__((aligned(16))) float xs[G][128];
   __shared__ float qp[G][128], us[G][128], csl[40];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int j = lane & 7, rs = lane >> 3;
-  // rows of this wave: P rows 32 w .. (w < 4), S P rows 32 (w - 4) .. (w >=
-  // 4); without P the first four waves read S P as well and drop the sums
-  const bool is_p = wave < 4;
+  // rows RPW w .. of [P; S P]; without P the waves of the P rows read S P
+  // as well and drop the sums
+  const bool is_p = wave * RPW < 128;
   const float* mat = (is_p && k.P) ? k.P : k.SP;
-  const int row0 = 32 * (wave & 3);
-  float4 a[4][4];
+  const int row0 = (wave * RPW) & 127;
+  float4 a[NPS][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < NPS; ++r)
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       a[r][c] = *reinterpret_cast<const float4*>(mat + (row0 + 8 * r + rs) * 128 + 4 * (8 * c + j));
@@ -780,7 +781,7 @@ __device__ __forceinline__ void build_p7_tables(P7Tables<G>& T, const P7Keys& k,
 #pragma unroll
     for (int c = 0; c < 4; ++c) x[c] = *reinterpret_cast<const float4*>(&xs[g][4 * (8 * c + j)]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < NPS; ++r) {
       float acc = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -1161,7 +1162,9 @@ __device__ __forceinline__ void quarter_sum(float s[G]) {
 // keys per pass of an NT-thread workgroup, NP passes per workgroup; the next
 // pass's words are loaded while the current pass is scored.  Grid (key
 // blocks, kv heads * head subgroups).
-template <int G, int NT, int NP>
+// FUSED: the query tables are built in the prologue from q, P and S P
+// (build_p7_tables) instead of read from k.qtab.
+template <int G, int NT, int NP, bool FUSED = false>
 __global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int cap, int gqa,
                                                           int n_sub, float scale) {
   constexpr int KPP = NT / 4, KPW = NP * KPP;  // keys per pass, per workgroup
@@ -1178,7 +1181,10 @@ __global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int c
   const uint32_t lim = static_cast<uint32_t>(last - blockIdx.x * KPW);
   P7Quarter A, B;
   load_p7_quarter(R, min(static_cast<uint32_t>(key), lim), qt, A);
-  load_p7_tables<G, NT>(T, k, h0);
+  if constexpr (FUSED)
+    build_p7_tables<G, NT>(T, k, h0);
+  else
+    load_p7_tables<G, NT>(T, k, h0);
   auto pass = [&](const P7Quarter& Q, int r) {
     float s[G];
     p7_quarter_score<G>(T, Q, qt, scale, s);
@@ -1925,10 +1931,10 @@ int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_
   P7Keys k;
   int st = p7_keys_setup(k, q_tables, angles, norms, qjl, cs_tables, num_heads, num_kv_heads, fn);
   if (st != TQ_OK) return st;
-  TQ_CHECK_ARG(scores != nullptr, "%s: scores is NULL", fn);
   TQ_CHECK_ARG(kv_len >= 0 && kv_capacity >= 1 && kv_len <= kv_capacity, "%s: bad kv_len", fn);
   TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
-  if (kv_len == 0) return TQ_OK;
+  if (kv_len == 0) return TQ_OK;  // nothing to write (scores may be NULL)
+  TQ_CHECK_ARG(scores != nullptr, "%s: scores is NULL", fn);
   k.scores = scores;
   const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, kP7MaxG), n_sub = gqa / G;
   TQ_CHECK_ARG(num_kv_heads * n_sub <= 65535, "%s: too many heads", fn);
@@ -1940,6 +1946,38 @@ int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_
   if (G == 1) polar7_score_kernel<1, NT, NP><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
   else polar7_score_kernel<2, NT, NP><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
   TQ_CHECK_LAUNCH("polar7_score_kernel");
+  return TQ_OK;
+}
+
+int tq_polar7_score_q(const float* q, const float* precondition, const float* sketch_precondition,
+                      const float* cs_tables, const uint32_t* angles, const uint32_t* norms,
+                      const uint32_t* qjl, int num_heads, int num_kv_heads, int kv_len,
+                      int kv_capacity, float scale, float* scores, void* stream) {
+  const char* fn = "tq_polar7_score_q";
+  TQ_CHECK_ARG(q && sketch_precondition && cs_tables && angles && norms && qjl, "%s: null pointer", fn);
+  TQ_CHECK_ARG(num_kv_heads >= 1 && num_heads >= num_kv_heads && num_heads % num_kv_heads == 0,
+               "%s: num_heads must be a multiple of num_kv_heads", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(angles) % 16 == 0 && reinterpret_cast<uintptr_t>(qjl) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(sketch_precondition) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(precondition) % 16 == 0,
+               "%s: angles / qjl / precondition / sketch_precondition must be 16-byte aligned", fn);
+  TQ_CHECK_ARG(kv_len >= 0 && kv_capacity >= 1 && kv_len <= kv_capacity, "%s: bad kv_len", fn);
+  TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
+  if (kv_len == 0) return TQ_OK;  // nothing to write (scores may be NULL)
+  TQ_CHECK_ARG(scores != nullptr, "%s: scores is NULL", fn);
+  P7Keys k{};
+  k.cs = cs_tables;
+  k.angles = angles; k.norms = norms; k.qjl = qjl;
+  k.q = q; k.P = precondition; k.SP = sketch_precondition;
+  k.scores = scores;
+  const int gqa = num_heads / num_kv_heads, G = polar_subgroup(gqa, kP7MaxG), n_sub = gqa / G;
+  TQ_CHECK_ARG(num_kv_heads * n_sub <= 65535, "%s: too many heads", fn);
+  constexpr int NT = 1024, NP = 8, KPW = NP * NT / 4;
+  dim3 grid((kv_len + KPW - 1) / KPW, num_kv_heads * n_sub);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (G == 1) polar7_score_kernel<1, NT, NP, true><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  else polar7_score_kernel<2, NT, NP, true><<<grid, NT, 0, s>>>(k, kv_len, kv_capacity, gqa, n_sub, scale);
+  TQ_CHECK_LAUNCH("polar7_score_kernel (fused query tables)");
   return TQ_OK;
 }
 

@@ -330,6 +330,22 @@ class Polar7Codec:
              _ptr(self.cs), Hq, Hkv, n, cap, float(scale), _ptr(out), _stream(stream))
         return out
 
+    def score_q(self, q: torch.Tensor, angles, norms, qjl, scale: float = 1.0, *,
+                kv_len: Optional[int] = None, stream=None) -> torch.Tensor:
+        """``score`` straight from the query q (Hq, 128) f32: every workgroup
+        builds its heads' query tables itself (one launch, no
+        ``prepare_query``)."""
+        _check_cuda("q", q)
+        _need(q.dim() == 2 and q.shape[1] == P7_D and q.dtype == torch.float32 and q.is_contiguous(),
+              "q must be contiguous (Hq, 128) f32")
+        Hq = q.shape[0]
+        Hkv, cap = angles.shape[0], angles.shape[1]
+        n = cap if kv_len is None else int(kv_len)
+        out = torch.empty((Hq, n), dtype=torch.float32, device=q.device)
+        call("tq_polar7_score_q", _ptr(q), _ptr(self.P), _ptr(self.SP), _ptr(self.cs), _ptr(angles),
+             _ptr(norms), _ptr(qjl), Hq, Hkv, n, cap, float(scale), _ptr(out), _stream(stream))
+        return out
+
     def sdpa_int4v(self, q_tables, angles, norms, qjl, v_quant, v_scales, v_biases,
                    scale: float = 1.0, sliding_window: int = 0, *, kv_len: Optional[int] = None,
                    out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:

@@ -362,6 +362,15 @@ int tq_polar7_prepare_query_sp(const float* q, const float* precondition,
 int tq_polar7_score(const float* q_tables, const uint32_t* angles, const uint32_t* norms,
                     const uint32_t* qjl, const float* cs_tables, int num_heads, int num_kv_heads,
                     int kv_len, int kv_capacity, float scale, float* scores, void* stream);
+/* The same scores straight from q [num_heads, 128] f32: each workgroup
+ * builds the query tables of its heads (as tq_polar7_prepare_query_sp) in
+ * its prologue, one launch in all (no counterpart in the reference, as
+ * above; compressed_score, lib/turboquant.h:157-165, also scores from the
+ * preconditioned query in one launch). */
+int tq_polar7_score_q(const float* q, const float* precondition, const float* sketch_precondition,
+                      const float* cs_tables, const uint32_t* angles, const uint32_t* norms,
+                      const uint32_t* qjl, int num_heads, int num_kv_heads, int kv_len,
+                      int kv_capacity, float scale, float* scores, void* stream);
 /* Decode attention over those scores (window rule and empty-set rule of
  * tq_sdpa_int4) with int4 V [num_kv_heads, kv_capacity, 16] + scale/bias
  * [.., 2] in sb_dtype; out [num_heads, 128] f32.  Workspace as

@@ -267,6 +267,24 @@ def test_polar7_score(pq, Hq, Hkv, L, scale):
     assert err.max() < SCORE_ATOL, f"max score err {err.max():.3e}"
 
 
+@pytest.mark.parametrize("Hq,Hkv,L,scale,rot", [(32, 16, 5000, 1.0, True), (4, 4, 333, 0.3, False),
+                                                (16, 2, 1200, 1.0, True), (8, 8, 70, 1.0, True),
+                                                (8, 2, 4096, 0.5, False)])
+def test_polar7_score_q(pq, Hq, Hkv, L, scale, rot):
+    """Scores straight from q (query tables built in each workgroup):
+    against the oracle and against the two-launch path."""
+    rng, codec, P, S, dk, hk, _ = p7_cache_on_gpu(pq, 7 * Hq + L, Hkv, L, rot=rot)
+    q = rng.standard_normal((Hq, 128)).astype(f32)
+    got = host(codec.score_q(dev(q), *dk, scale))
+    tab, qp, qs = codec.prepare_query(dev(q), with_vectors=True)
+    two = host(codec.score(tab, *dk, scale))
+    assert np.max(np.abs(got - two)) < 1e-4, f"fused vs two-launch {np.max(np.abs(got - two)):.3e}"
+    ref = PQ.polar7_scores(host(qp), host(qs), hk[0], host_norms(hk[1]), hk[2], Hq // Hkv, scale)
+    err = np.abs(got - ref)
+    assert err.max() < SCORE_ATOL, f"max score err {err.max():.3e}"
+    assert codec.score_q(dev(q), *dk, scale, kv_len=0).shape == (Hq, 0)
+
+
 @pytest.mark.parametrize("Hq,Hkv,L,W,sb", [
     (32, 16, 786, 0, "f16"), (32, 16, 3000, 1024, "f16"), (4, 4, 1, 0, "f32"),
     (8, 1, 5000, 0, "f16"), (16, 2, 20000, 0, "f16"), (2, 2, 400, 0, "f32")])
