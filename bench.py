@@ -426,6 +426,27 @@ def bench_stream(args, torch, tq, O, gen, Hq, Hkv, D):
         tiles.append({"waves": waves, "loads_per_lane": u, "depth": depth, "nt": nt,
                       "blocks": blocks, "us": round(ms_p * 1e3, 2),
                       "gbs": round(hl / (ms_p * 1e-3) / 1e9, 1)})
+    # the floor at the sliding layer's size (configs[1], 16 x 786 x 288 B):
+    # one workgroup per kv head (a single pass, no split merge) up to the
+    # planner's split counts and beyond.  A launch this short is shorter
+    # than a Python call, so 50 launches (rotated windows) are one HIP
+    # graph, as in the sliding50 workload, and a launch is a replay / 50.
+    small = Hkv * 786 * 288
+    nwin_s = nbytes // (small + 4096)
+    small_floor = []
+    for blocks in (Hkv, 2 * Hkv, 4 * Hkv, 7 * Hkv, ncu):
+        for waves, u, depth in ((8, 4, 1), (8, 4, 3), (8, 9, 2), (8, 16, 1), (16, 4, 3), (16, 9, 1)):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(50):
+                    _lib.call("tq_stream_read_tiles",
+                              ctypes.c_void_p(a.data_ptr() + (i % nwin_s) * (small + 4096)), small,
+                              ctypes.c_void_p(sink.data_ptr()), blocks, waves, u, depth, 1, sptr())
+            ms_p, _, _ = time_launches(torch, lambda i: g.replay(), max(5, args.steps // 50),
+                                       max(2, args.warmup // 50))
+            del g
+            small_floor.append({"blocks": blocks, "waves": waves, "loads_per_lane": u, "depth": depth,
+                                "us": round(ms_p * 1e3 / 50, 2)})
     del a
     torch.cuda.empty_cache()
     # the attention launch itself, same box, same rotation rule
@@ -446,6 +467,7 @@ def bench_stream(args, torch, tq, O, gen, Hq, Hkv, D):
           "attention_us_same_box": round(ms_attn * 1e3, 2),
           "attention_over_best_probe": round(ms_attn * 1e3 / best["us"], 4),
           "torch_sum_1GiB_gbs": round(read_gbs, 1), "torch_copy_1GiB_gbs": round(copy_gbs, 1),
+          "sliding_layer_bytes": small, "sliding_layer_sweep": small_floor,
           "config": {"workload": "streaming read probes over 151,044,096 B, rotated windows",
                      "global_batch": 1, "seq_len": 32768, "parallelism": "none (1 GPU)"}}, args)
 
