@@ -720,9 +720,28 @@ __device__ __forceinline__ int p7_t1_row(int row) {
 template <int G, int NT>
 __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0) {
   constexpr int kVec = kP7QTab / 4;
-  for (int i = threadIdx.x; i < G * kVec; i += NT) {
+  // every 16-byte load first (one memory round trip), then the LDS stores:
+  // a load-then-store loop would wait a round trip per iteration
+  constexpr int NV = (G * kVec + NT - 1) / NT;
+  const float4* src = reinterpret_cast<const float4*>(k.qtab + static_cast<int64_t>(h0) * kP7QTab);
+  float4 vv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = min(static_cast<int>(threadIdx.x) + j * NT, G * kVec - 1);  // clamped; dropped below
+    vv[j] = src[i];  // head h0 + i / kVec, entry i % kVec: the G heads' tables are adjacent
+  }
+  // the level-pair factors of lane (kp, k0, k1) of the first wave, loaded
+  // with the tables
+  const int kp = threadIdx.x & 3, k0 = (threadIdx.x >> 2) & 3, k1 = (threadIdx.x >> 4) & 3;
+  const float* c2 = k.cs + 32;  // (cos, sin) pairs; 4-byte alignment only
+  const float2 cpp = make_float2(c2[2 * kp], c2[2 * kp + 1]), c0p = make_float2(c2[2 * k0], c2[2 * k0 + 1]),
+               c1p = make_float2(c2[2 * k1], c2[2 * k1 + 1]);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = static_cast<int>(threadIdx.x) + j * NT;
+    if (i >= G * kVec) break;
     const int g = i / kVec, r = i - (i / kVec) * kVec;
-    const float4 v = reinterpret_cast<const float4*>(k.qtab + static_cast<int64_t>(h0 + g) * kP7QTab)[r];
+    const float4 v = vv[j];
     const float f[4] = {v.x, v.y, v.z, v.w};
     if (r < 256) {
       const int row = p7_t1_row(r >> 2), c0 = 4 * (r & 3);
@@ -735,13 +754,8 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
     }
     else if (r == 1280) T.U[g] = (v.x + v.y) + (v.z + v.w);
   }
-  if (threadIdx.x < 64) {
-    const int kp = threadIdx.x & 3, k0 = (threadIdx.x >> 2) & 3, k1 = threadIdx.x >> 4;
-    const float* c2 = k.cs + 32;
-    const float cp = c2[2 * kp], sp = c2[2 * kp + 1];
-    T.t2[threadIdx.x] = make_float4(cp * c2[2 * k0], cp * c2[2 * k0 + 1], sp * c2[2 * k1],
-                                    sp * c2[2 * k1 + 1]);
-  }
+  if (threadIdx.x < 64)
+    T.t2[threadIdx.x] = make_float4(cpp.x * c0p.x, cpp.x * c0p.y, cpp.y * c1p.x, cpp.y * c1p.y);
   __syncthreads();
 }
 
