@@ -1297,6 +1297,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
     for (int u = 0; u < 4; ++u) load_sub(key[u], base0, u);
   }
+  __shared__ int s_done[NW];  // tiles processed, per wave (issue pacing)
+  if (lane == 0) s_done[wave] = 0;  // published by the tables' barrier
   if constexpr (FUSED)
     build_p7_tables<G, NW * 64>(T, k, h0);
   else
@@ -1440,9 +1442,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     wave_lds_sync();
   };
 
+  // the two waves of a SIMD kept level: the one behind issues first (its
+  // priority raised), so they end their tiles together rather than ~4.5 us
+  // apart, the later one alone on the SIMD
+  pace_waves<NW>(s_done, wv, lane, 0);
   for (int it = 0; it < ntile; ++it) {
     const int tb = base0 + it * NW * 64;
     process(tb, min(tb + NW * 64, last));
+    pace_waves<NW>(s_done, wv, lane, it + 1);
   }
 
   // columns: sum the four K-slot groups; lane (vm, vc) holds V words
