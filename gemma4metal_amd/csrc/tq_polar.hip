@@ -717,8 +717,8 @@ __device__ __forceinline__ int p7_t1_row(int row) {
 // four grandchild factors of a pair with code kp whose child pairs have
 // codes k0, k1 (two levels of the top-down decode per lookup).  All NT
 // threads call it; it ends with a barrier.
-template <int G, int NT>
-__device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0) {
+template <int G, int NT, typename AfterLoads>
+__device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0, AfterLoads&& after_loads) {
   constexpr int kVec = kP7QTab / 4;
   // every 16-byte load first (one memory round trip), then the LDS stores:
   // a load-then-store loop would wait a round trip per iteration
@@ -736,6 +736,9 @@ __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, 
   const float* c2 = k.cs + 32;  // (cos, sin) pairs; 4-byte alignment only
   const float2 cpp = make_float2(c2[2 * kp], c2[2 * kp + 1]), c0p = make_float2(c2[2 * k0], c2[2 * k0 + 1]),
                c1p = make_float2(c2[2 * k1], c2[2 * k1 + 1]);
+  // the caller's first key loads go out behind the tables' (which are
+  // needed first)
+  after_loads();
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int i = static_cast<int>(threadIdx.x) + j * NT;
@@ -1193,12 +1196,18 @@ __global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int c
   // rows of this workgroup: rowbase + blockIdx.x * KPW + (0 .. lim)
   const P7Rows R = p7_rows(k, rowbase + blockIdx.x * KPW);
   const uint32_t lim = static_cast<uint32_t>(last - blockIdx.x * KPW);
+  __shared__ int s_done[NT / 64];  // passes done, per wave (issue pacing)
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  if (lane == 0) s_done[wv] = 0;  // published by the tables' barrier
   P7Quarter A, B;
-  load_p7_quarter(R, min(static_cast<uint32_t>(key), lim), qt, A);
-  if constexpr (FUSED)
+  auto first = [&]() { load_p7_quarter(R, min(static_cast<uint32_t>(key), lim), qt, A); };
+  if constexpr (FUSED) {
+    first();
     build_p7_tables<G, NT>(T, k, h0);
-  else
-    load_p7_tables<G, NT>(T, k, h0);
+  } else {
+    load_p7_tables<G, NT>(T, k, h0, first);
+  }
   auto pass = [&](const P7Quarter& Q, int r) {
     float s[G];
     p7_quarter_score<G>(T, Q, qt, scale, s);
@@ -1211,11 +1220,17 @@ __global__ __launch_bounds__(NT) void polar7_score_kernel(P7Keys k, int n, int c
       k.scores[static_cast<int64_t>(h0 + qt) * n + t] = v;
     }
   };
+  // the four waves of a SIMD kept level (see pace_waves)
+  pace_waves<NT / 64>(s_done, wv, lane, 0);
   for (int r = 0; r < npass; r += 2) {
     load_p7_quarter(R, min(static_cast<uint32_t>(key + KPP * (r + 1)), lim), qt, B);
     pass(A, r);
+    pace_waves<NT / 64>(s_done, wv, lane, r + 1);
     load_p7_quarter(R, min(static_cast<uint32_t>(key + KPP * (r + 2)), lim), qt, A);
-    if (r + 1 < npass) pass(B, r + 1);
+    if (r + 1 < npass) {
+      pass(B, r + 1);
+      pace_waves<NT / 64>(s_done, wv, lane, r + 2);
+    }
   }
 }
 
@@ -1293,16 +1308,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const P7Rows R = p7_rows(k, rowbase + tb);
     load_p7_quarter(R, min(static_cast<uint32_t>(16 * u + kq), static_cast<uint32_t>(last - tb)), qt, Q);
   };
-  if (ntile > 0) {
+  auto first = [&]() {
+    if (ntile > 0) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load_sub(key[u], base0, u);
-  }
+      for (int u = 0; u < 4; ++u) load_sub(key[u], base0, u);
+    }
+  };
   __shared__ int s_done[NW];  // tiles processed, per wave (issue pacing)
   if (lane == 0) s_done[wave] = 0;  // published by the tables' barrier
-  if constexpr (FUSED)
+  if constexpr (FUSED) {
+    first();
     build_p7_tables<G, NW * 64>(T, k, h0);
-  else
-    load_p7_tables<G, NW * 64>(T, k, h0);
+  } else {
+    load_p7_tables<G, NW * 64>(T, k, h0, first);
+  }
 
   float m_run[G], l_run[G];
 #pragma unroll

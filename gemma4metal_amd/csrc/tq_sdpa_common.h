@@ -283,6 +283,22 @@ __device__ __forceinline__ void pace_waves(int* done_lds, int wv, int lane, int 
       __builtin_amdgcn_s_setprio(1);
     else
       __builtin_amdgcn_s_setprio(0);
+  } else if constexpr (NW == 16) {
+    // four waves per SIMD (w, w + 4, w + 8, w + 12): a wave behind the
+    // furthest of its partners takes priority 1, or 2 when two or more
+    // steps behind
+    if (lane == 0) __hip_atomic_store(&done_lds[wv], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int mx = done;
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      mx = max(mx, __hip_atomic_load(&done_lds[(wv + 4 * j) & 15], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    const int behind = __builtin_amdgcn_readfirstlane(mx) - done;
+    if (behind >= 2)
+      __builtin_amdgcn_s_setprio(2);
+    else if (behind == 1)
+      __builtin_amdgcn_s_setprio(1);
+    else
+      __builtin_amdgcn_s_setprio(0);
   }
 }
 
