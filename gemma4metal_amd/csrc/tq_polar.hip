@@ -715,8 +715,10 @@ __device__ __forceinline__ int p7_t1_row(int row) {
 // combined two-level table t2[kp | k0 << 2 | k1 << 4] = (cos_p cos_0,
 // cos_p sin_0, sin_p cos_1, sin_p sin_1) of the levels 2-7 codebook: the
 // four grandchild factors of a pair with code kp whose child pairs have
-// codes k0, k1 (two levels of the top-down decode per lookup).  All NT
-// threads call it; it ends with a barrier.
+// codes k0, k1 (two levels of the top-down decode per lookup).
+// `after_loads()` runs once the tables' loads are issued (the caller's first
+// key loads go there, behind them).  All NT threads call it; it ends with a
+// barrier.
 template <int G, int NT, typename AfterLoads>
 __device__ __forceinline__ void load_p7_tables(P7Tables<G>& T, const P7Keys& k, int h0, AfterLoads&& after_loads) {
   constexpr int kVec = kP7QTab / 4;
