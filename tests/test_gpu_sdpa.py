@@ -221,6 +221,43 @@ def test_workspace_reuse_across_shapes(gpu):
             assert_close(host(out), ref, f"rep {rep} case {i}")
 
 
+def test_workspace_shared_by_both_merge_forms(gpu):
+    """One workspace serving, in turn, D=512 calls (split partials merged by
+    a second launch) and calls whose last workgroup merges them (D=256
+    decode, a ragged batch, D=128): the partial slots overlap, and whatever
+    one form leaves there must not leak into the other's results."""
+    rng = np.random.default_rng(77)
+    q512, v512 = queries(rng, (32, 512), "bf16")
+    c512 = host_cache(rng, 4, 5000, 512)
+    r512 = O.sdpa_int4(v512, *c512, 8, 1.0, 0)
+    q256, v256 = queries(rng, (32, 256), "bf16")
+    c256 = host_cache(rng, 16, 4000, 256)
+    r256 = O.sdpa_int4(v256, *c256, 2, 1.0, 0)
+    q128, v128 = queries(rng, (8, 128), "f32")
+    c128 = host_cache(rng, 4, 3000, 128)
+    r128 = O.sdpa_int4(v128, *c128, 2, 1.0, 0)
+    lens, wins = [3000, 1, 2100], [0, 0, 1024]
+    qr, vr = queries(rng, (3, 32, 256), "bf16")
+    k = O.rms_norm(rng.standard_normal((3, 16, 3000, 256)).astype(np.float32))
+    v = rng.standard_normal((3, 16, 3000, 256)).astype(np.float32)
+    cr = O.quantize_int4(k) + O.quantize_int4(v)
+    rr = O.sdpa_int4_ragged(vr, *cr, np.array(lens), np.array(wins), 2)
+    d512, d256, d128, dr = ([dev(a) for a in c] for c in (c512, c256, c128, cr))
+    ld, wd = dev(np.array(lens, np.int32)), dev(np.array(wins, np.int32))
+    assert gpu.sdpa_plan(32, 4, 512, 5000)["kernel"] == "sdpa_int4_hc2_kernel"
+    for rep in range(3):
+        for what in ("512", "256", "512", "ragged", "128", "512", "512", "256"):
+            if what == "512":
+                got, ref = gpu.sdpa_int4(q512, *d512, 8, 1.0, 0), r512
+            elif what == "256":
+                got, ref = gpu.sdpa_int4(q256, *d256, 2, 1.0, 0), r256
+            elif what == "128":
+                got, ref = gpu.sdpa_int4(q128, *d128, 2, 1.0, 0), r128
+            else:
+                got, ref = gpu.sdpa_int4_ragged(qr, *dr, ld, 2, windows=wd), rr
+            assert_close(host(got), ref, f"rep {rep} {what}")
+
+
 @pytest.mark.parametrize("Hq,Hkv,L,W,qdt", [
     (32, 4, 5000, 0, "bf16"),     # Gemma global layer: many splits, partial last iteration
     (32, 4, 3001, 1024, "bf16"),  # window active
