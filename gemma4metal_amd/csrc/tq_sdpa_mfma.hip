@@ -240,10 +240,9 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int col_hi = pos;
   const int col_lo = p.window > 0 ? pos - p.window + 1 : 0;
 
-  // With packed columns each wave leaves two partial results, the hi- and
-  // lo-part columns' products (slots wave and wave + NW), summed by the
-  // workgroup merge.
-  using Fin = Finalize<G, D, PACK ? 2 * NW : NW, NW * 64>;
+  // One partial result per wave (with packed columns the hi- and lo-part
+  // columns' products are summed in registers first).
+  using Fin = Finalize<G, D, NW, NW * 64>;
   __shared__ __align__(16) float arena[Fin::kArena];
   // scales staged per wave as [array][group][key pair] fp16x2, or
   // [array][group][key] fp32
@@ -671,13 +670,13 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   bacc = xor32_sum(bacc);
   if constexpr (PACK) {
     // columns n and n + 8 hold tile 0's / tile 1's keys (denominator, bias
-    // term): add the two; the hi / lo weight parts' products stay in their
-    // own lanes and arena slots, each with its own 128 offset removed
+    // term): add the two; the hi / lo weight parts' products are added
+    // below, each with its own 128 offset removed
     l_sum += ror8(l_sum);
     bacc += ror8(bacc);
-    if (T) bacc = 0.0f;  // counted once, in the hi-part slot
+    if (T) bacc = 0.0f;  // counted once, in the hi part
   }
-  const int slot = wave + (PACK ? T * NW : 0);
+  const int slot = wave;
   if (col_used) {
     // Accumulator element (s, j) of C row 4c + i is dim 8 * (VW * (4c + i) +
     // s) + j: for one (c, i) the 8 * VW dims are contiguous and lie in one
@@ -699,17 +698,22 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
 #pragma unroll
             for (int s2 = 0; s2 < VWH; ++s2)
               if (s2 == so) v = (cv[8 * s2 + j][i] - 128.0f * wsum) + bacc;
+            // packed: lane m + 8 holds the lo part of lane m's column (the
+            // pair agrees on every branch here)
+            if constexpr (PACK) v += ror8(v);
             row[8 * sg + j] = v;
           }
         v4f* dst = reinterpret_cast<v4f*>(Fin::o(arena, slot, hn) + dim0);
+        if (T == 0) {
 #pragma unroll
-        for (int q4 = 0; q4 < 2 * VW; ++q4)
-          dst[q4] = v4f{row[4 * q4], row[4 * q4 + 1], row[4 * q4 + 2], row[4 * q4 + 3]};
+          for (int q4 = 0; q4 < 2 * VW; ++q4)
+            dst[q4] = v4f{row[4 * q4], row[4 * q4 + 1], row[4 * q4 + 2], row[4 * q4 + 3]};
+        }
       }
     }
-    if (gn == 0 && c == 0) {
+    if (gn == 0 && c == 0 && T == 0) {
       Fin::m(arena, slot)[hn] = m_run;
-      Fin::l(arena, slot)[hn] = (vhalf == 0 && T == 0) ? l_sum : 0.0f;
+      Fin::l(arena, slot)[hn] = vhalf == 0 ? l_sum : 0.0f;
     }
   }
   if constexpr (kQG)
