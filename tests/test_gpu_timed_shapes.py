@@ -127,6 +127,47 @@ def test_sliding50_graph_step(gpu):
         assert_close(eager[i], ref, f"layer {i}")
 
 
+def test_mixed_layers_graph_step(gpu):
+    """A Gemma-like decode step in one HIP graph: sliding layers (D 256,
+    last-workgroup merge) around a global layer (D 512, the heads-as-columns
+    kernel and the separate merge launch), all on one workspace.  Replays
+    equal the eager step bit for bit; the global layer matches the oracle."""
+    g = torch.Generator(device="cuda").manual_seed(4512)
+    rng = np.random.default_rng(4512)
+    slid = [gpu_cache(gpu, 16, 786, 256, g) for _ in range(3)]
+    glob = gpu_cache(gpu, 4, 4096, 512, g)
+    assert gpu.sdpa_plan(32, 4, 512, 4096)["kernel"] == "sdpa_int4_hc2_kernel"
+    assert gpu.sdpa_plan(32, 4, 512, 4096)["splits"] > 1
+    qs, _ = queries(rng, (32, 256), "bf16")
+    qg, qgv = queries(rng, (32, 512), "bf16")
+    outs = [torch.empty((32, 256), dtype=torch.float32, device="cuda") for _ in range(3)]
+    outg = torch.empty((32, 512), dtype=torch.float32, device="cuda")
+
+    def step():
+        gpu.sdpa_int4(qs, *slid[0], 2, 1.0, 1024, out=outs[0])
+        gpu.sdpa_int4(qs, *slid[1], 2, 1.0, 1024, out=outs[1])
+        gpu.sdpa_int4(qg, *glob, 8, 1.0, 0, out=outg)
+        gpu.sdpa_int4(qs, *slid[2], 2, 1.0, 1024, out=outs[2])
+
+    step()
+    torch.cuda.synchronize()
+    eager = [host(o).copy() for o in outs + [outg]]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for rep in range(3):
+        for o in outs + [outg]:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs + [outg]):
+            assert np.array_equal(host(o), eager[i]), f"replay {rep} output {i}"
+        # eager work on the same workspace between replays
+        gpu.sdpa_int4(qg, *glob, 8, 1.0, 0, out=outg)
+        torch.cuda.synchronize()
+    check_heads(eager[3], qgv, glob, (1,), 8, what="global layer in the graph")
+
+
 def test_ragged_full_size_append_then_attend(gpu):
     """configs[3] at full size, as bench.py times it: B 64, lengths
     U[512, 32768] (seed 4), W 1024 on even sequences, capacity 32769; one
