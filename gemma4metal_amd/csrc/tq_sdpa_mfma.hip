@@ -266,7 +266,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const uint32_t* sc_arr = static_cast<const uint32_t*>(sc_base) + row0 * Gm::SCW;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   // wave wv streams keys with the NWK waves of its V half (wv / NWK)
-  const int vhalf = wv / NWK;
+  const int vhalf = VS == 1 ? 0 : wv / NWK;  // (a constant without a V split)
   LaneOffs lo;
   lo.k = m * (D / 2) + c * Gm::KW * 4;
   lo.v = 4 * c * (D / 2) + (m * Gm::VW + vhalf * Gm::VWH) * 4;
@@ -677,6 +677,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     if (T) bacc = 0.0f;  // counted once, in the hi part
   }
   const int slot = wave;
+  const float corr = bacc - 128.0f * wsum;  // bias term and the 128 offset
   if (col_used) {
     // Accumulator element (s, j) of C row 4c + i is dim 8 * (VW * (4c + i) +
     // s) + j: for one (c, i) the 8 * VW dims are contiguous and lie in one
@@ -697,7 +698,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
             float v = 0.0f;
 #pragma unroll
             for (int s2 = 0; s2 < VWH; ++s2)
-              if (s2 == so) v = (cv[8 * s2 + j][i] - 128.0f * wsum) + bacc;
+              if (s2 == so) v = cv[8 * s2 + j][i] + corr;
             // packed: lane m + 8 holds the lo part of lane m's column (the
             // pair agrees on every branch here)
             if constexpr (PACK) v += ror8(v);
