@@ -302,9 +302,10 @@ __device__ __forceinline__ void pace_waves(int* done_lds, int wv, int lane, int 
   }
 }
 
-// LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G], later
-// reused for the per-split (m, l) of the last workgroup.  NW = partial
-// results per workgroup (one per wave, or per key stream), NT = threads.
+// LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G] (sized to
+// at least 2*G*kMaxSplits floats, room for per-split (m, l) pairs).  NW =
+// partial results per workgroup (one per wave, or per key stream), NT =
+// threads.
 template <int G, int D, int NW = kWaves, int NT = NW * 64>
 struct Finalize {
   static constexpr int kNT = NT;
