@@ -1146,21 +1146,24 @@ __device__ __forceinline__ void p7_quarter_score(const P7Tables<G>& T, const P7Q
     // mask of the raw word (two instructions per lookup instead of none)
     asm("" : "+v"(lo[w]), "+v"(hi[w]));
   }
+  // all 16 level-1 entries first (one aligned G-float read each, ds_read_b64
+  // at G = 2 with the constant in its offset field), then the products
+  typedef float vGf __attribute__((ext_vector_type(G)));
+  vGf ents[16];
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const int ii = jj >> 2, e = jj & 3, n = jj % 8;
+    const uint32_t src = (n & 1) ? hi[jj >> 3] : lo[jj >> 3];
+    const uint32_t off = (src >> (8 * (n >> 1))) & 0xFFu;
+    ents[jj] = *reinterpret_cast<const vGf*>(t1r[e] + ii * (4 * 16 * kE) + off);
+  }
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
     const float r1[4] = {r3[ii] * tc[ii].x, r3[ii] * tc[ii].y, r3[ii] * tc[ii].z, r3[ii] * tc[ii].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int jj = 4 * ii + e;  // level-1 pair 16 qt + jj: nibble jj % 8 of word jj / 8
-      const int n = jj % 8;
-      const uint32_t src = (n & 1) ? hi[jj >> 3] : lo[jj >> 3];
-      const uint32_t off = (src >> (8 * (n >> 1))) & 0xFFu;
-      // one aligned G-float read (ds_read_b64 at G = 2, with the constant in
-      // its offset field)
-      typedef float vGf __attribute__((ext_vector_type(G)));
-      const vGf ent = *reinterpret_cast<const vGf*>(t1r[e] + ii * (4 * 16 * kE) + off);
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = fmaf(r1[e], ent[g], acc[g]);
+      for (int g = 0; g < G; ++g) acc[g] = fmaf(r1[e], ents[4 * ii + e][g], acc[g]);
     }
   }
   const float cr = kQjlCoef * rn;
