@@ -315,10 +315,14 @@ def main():
         def one_step():
             for s in sets:
                 tq.sdpa_int4(q, *s, Hq // Hkv, 1.0, W, out=out)
-        one_step()
+        # warm the capture stream up eagerly, so its split-K workspace exists
+        # before capture (nothing is allocated inside the graph)
+        cs = torch.cuda.Stream()
+        with torch.cuda.stream(cs):
+            one_step()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=cs):
             one_step()
         ms_step, ms_launch, _ = time_launches(torch, lambda i: g.replay(), args.steps, args.warmup)
         us_layer = ms_step * 1e3 / layers

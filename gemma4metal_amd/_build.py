@@ -17,7 +17,9 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libturboquant_hip.so")
-ARCH = os.environ.get("TQ_OFFLOAD_ARCH", "gfx950")
+# gfx950 only: the decode kernels' split-K merge protocol rests on gfx950's
+# memory behaviour (tq_sdpa_common.h refuses any other device target too).
+ARCH = "gfx950"
 
 HIP_SOURCES = ["tq_runtime.hip", "tq_quant.hip", "tq_sdpa.hip", "tq_sdpa_mfma.hip", "tq_sdpa_hc.hip",
                "tq_prefill.hip", "tq_polar.hip"]

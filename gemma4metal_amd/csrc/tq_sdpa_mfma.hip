@@ -275,10 +275,11 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int nit = base0 < t_end ? (t_end - base0 + kIter - 1) / kIter : 0;
   // First row of the 32-row block read for the iteration at key t0: t0
   // itself while the block lies below t_end; else moved back to end at
-  // t_end (rows of the split, the keys before t0 masked in process), and to
-  // row 0 for splits ending before row 32.  Rows stay in [0, max(t_end,
-  // 32)), inside the cache: the planner gives this kernel capacities of at
-  // least 32 rows.  Wave-uniform (scalar).
+  // t_end (rows of the sequence, the keys before t0 masked in process), and
+  // to row 0 for sequences shorter than 32 keys, whose rows [t_end, 32) lie
+  // past the sequence (process zeroes their scales and biases).  Rows stay
+  // in [0, max(t_end, 32)), inside the cache: the planner gives this kernel
+  // capacities of at least 32 rows.  Wave-uniform (scalar).
   auto block_row = [&](int t0) { return max(0, min(t0, t_end - 32)); };
 
   // q is loaded first: at kernel start every workgroup issues its K/V stream
@@ -411,13 +412,31 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     issue(std::integral_constant<int, 0>{});
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t n_keep = static_cast<uint32_t>(t_end - t0);  // > 0 for a processed iteration
+    // This lane's scale words (keys r0 + 2 k16, r0 + 2 k16 + 1).  A sequence
+    // shorter than one block reads rows [t_end, 32) too (block_row moves the
+    // block to row 0): rows past the sequence, possibly never written.  Their
+    // keys get zero weight, but 0 * NaN is NaN, so their scales and biases
+    // are replaced by zero before any product sees them.
+    uint32_t scv[2][Gm::SCW];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int w = 0; w < Gm::SCW; ++w) scv[e][w] = B.sc[e][w];
+    if (t_end < 32) {  // uniform, and rare: only then can a block row pass t_end
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const bool in_seq = r0 + 2 * k16 + e < t_end;
+#pragma unroll
+        for (int w = 0; w < Gm::SCW; ++w) scv[e][w] = in_seq ? scv[e][w] : 0u;
+      }
+    }
     // scales -> LDS [array][group][key]
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       if constexpr (F32) {
-        *reinterpret_cast<uint2*>(&sc_lds[wv][arr][g][2 * k16]) = uint2{B.sc[0][g], B.sc[1][g]};
+        *reinterpret_cast<uint2*>(&sc_lds[wv][arr][g][2 * k16]) = uint2{scv[0][g], scv[1][g]};
       } else {
-        const uint32_t a0 = B.sc[0][g >> 1], a1 = B.sc[1][g >> 1];
+        const uint32_t a0 = scv[0][g >> 1], a1 = scv[1][g >> 1];
         const uint32_t v = (g & 1) ? ((a0 >> 16) | (a1 & 0xFFFF0000u))
                                    : ((a0 & 0xFFFFu) | (a1 << 16));
         sc_lds[wv][arr][g][k16] = v;

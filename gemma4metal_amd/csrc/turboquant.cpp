@@ -70,6 +70,17 @@ void* workspace(size_t bytes, size_t* have, StreamOrDevice s) {
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   Workspace& w = g_ws[{dev, stream}];
   if (w.bytes < bytes) {
+    // Growing records an allocation, a fill and a free: under stream capture
+    // they would become graph nodes, and the graph would own the buffer this
+    // map keeps.  Refuse instead of recording them.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    check_hip(hipStreamIsCapturing(stream, &cap), "hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone)
+      throw std::runtime_error(
+          "turboquant: the split-K workspace of this (device, stream) must grow, but the stream "
+          "is being captured; make one eager call of the largest shape on this stream before "
+          "capture, pass a workspace (sdpa_int4_into with workspace), or use "
+          "tq_sdpa_int4_noalloc");
     const size_t nb = std::max<size_t>(bytes, size_t{1} << 20);
     void* p = nullptr;
     check_hip(hipMallocAsync(&p, nb, stream), "hipMallocAsync");

@@ -68,13 +68,19 @@ def workspace(nbytes: int, device: torch.device, stream_handle: int) -> torch.Te
     allocated and zero-filled on that stream (torch's allocator then orders
     its reuse after the stream's queued work), so the fill is ordered before
     the kernels that use it, and a replaced buffer is released only behind
-    the calls already queued there.  The first call on a (device, stream)
-    must not be under graph capture (tq_sdpa_int4_noalloc serves such
-    callers)."""
+    the calls already queued there.  A buffer cannot be created or grown
+    under graph capture (the graph would own the allocation): that raises,
+    so the caller warms the capture stream up eagerly with the largest shape
+    first (``torch.cuda.graph(g, stream=s)`` after a call on ``s``), or uses
+    tq_sdpa_int4_noalloc."""
     dev = device.index if device.index is not None else torch.cuda.current_device()
     key = (dev, stream_handle)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        _need(not torch.cuda.is_current_stream_capturing(),
+              "the split-K workspace of this (device, stream) must be created or grown, but the "
+              "stream is being captured: call once eagerly on the capture stream first "
+              "(torch.cuda.graph(g, stream=s)), or use tq_sdpa_int4_noalloc")
         s = torch.cuda.ExternalStream(stream_handle, device=torch.device("cuda", dev))
         with torch.cuda.stream(s):
             ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

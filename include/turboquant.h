@@ -76,7 +76,10 @@ array sdpa_int4(const array& queries, const array& k_quant, const array& k_scale
 
 // The same into a caller-owned output, over rows [0, kv_len) of caches whose
 // row stride is k_quant.shape(1) (kv_len < 0: all rows).  The split-K
-// workspace is the library's buffer for the calling (device, stream).
+// workspace is the library's buffer for the calling (device, stream); it
+// grows with stream-ordered allocations, so under stream (graph) capture a
+// call that would grow it throws: make one eager call of the largest shape on
+// that stream first, or use the overload below.
 void sdpa_int4_into(array& out, const array& queries, const array& k_quant,
                     const array& k_scales, const array& k_biases, const array& v_quant,
                     const array& v_scales, const array& v_biases, int gqa_factor,

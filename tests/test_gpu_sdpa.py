@@ -633,3 +633,52 @@ def test_fresh_workspace_on_non_default_streams(gpu):
     torch.cuda.synchronize()
     for kind, o in outs:
         assert np.array_equal(host(o), ref_d if kind == "d" else ref_r), kind
+
+
+def _poison_tail(c, n_valid, sb):
+    """Returns device copies of cache c whose rows from n_valid on hold
+    non-finite scales and biases (rows past the sequence, never written by
+    an append): K scale +Inf, K bias NaN, V scale NaN, V bias -Inf."""
+    kq, ks, kb, vq, vs, vb = [a.copy() for a in c]
+    if sb == "f16":
+        nan, inf = np.uint16(0x7E00).view(np.float16), np.float16(np.inf)
+    else:
+        nan, inf = np.float32(np.nan), np.float32(np.inf)
+    ks[..., n_valid:, :] = inf
+    kb[..., n_valid:, :] = nan
+    vs[..., n_valid:, :] = nan
+    vb[..., n_valid:, :] = -inf
+    return [dev(a) for a in (kq, ks, kb, vq, vs, vb)]
+
+
+@pytest.mark.parametrize("sb", ["f16", "f32"])
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 16, 256), (8, 4, 128), (8, 4, 512)])
+@pytest.mark.parametrize("n", [1, 17, 31])
+def test_short_sequence_unwritten_tail(gpu, sb, Hq, Hkv, D, n):
+    """A sequence shorter than one 32-key block in a cache of 64 rows: rows
+    past it (never written) hold NaN / Inf scales and biases, and the output
+    still matches the oracle over the first n rows -- decode (kv_len),
+    ragged (seq_lens) and prefill (causal end inside the first block)."""
+    rng = np.random.default_rng(900 + n + D)
+    cap = 64
+    c = host_cache(rng, Hkv, cap, D, sb)
+    cd = _poison_tail(c, n, sb)
+    qd, qv = queries(rng, (Hq, D), "bf16")
+    out = gpu.sdpa_int4(qd, *cd, Hq // Hkv, 1.0, 0, kv_len=n)
+    cut = [a[:, :n] for a in c]
+    assert_close(host(out), O.sdpa_int4(qv, *cut, Hq // Hkv, 1.0, 0), f"decode n={n}")
+    # ragged: every sequence of the batch ends at n (caches (B, Hkv, cap, .))
+    B = 2
+    cb = [np.stack([a, a]) for a in c]
+    cbd = _poison_tail(cb, n, sb)
+    lens = np.full(B, n, np.int32)
+    qr, qrv = queries(rng, (B, Hq, D), "bf16")
+    out_r = gpu.sdpa_int4_ragged(qr, *cbd, dev(lens), Hq // Hkv)
+    ref_r = O.sdpa_int4_ragged(qrv, *cb, lens, np.zeros(B, np.int32), Hq // Hkv)
+    assert_close(host(out_r), ref_r, f"ragged n={n}")
+    # prefill: queries at positions n - S .. n - 1 over rows [0, n)
+    S = min(n, 5)
+    qp, qpv = queries(rng, (S, Hq, D), "bf16")
+    out_p = gpu.sdpa_int4_prefill(qp, *cd, n - S, Hq // Hkv, 1.0, 0)
+    ref_p = O.sdpa_int4_prefill(qpv, *c, n - S, Hq // Hkv, 1.0, 0)
+    assert_close(host(out_p), ref_p, f"prefill n={n}")

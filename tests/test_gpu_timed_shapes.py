@@ -93,8 +93,8 @@ def test_sweep_points(gpu, L):
 def test_sliding50_graph_step(gpu):
     """configs[1] as bench.py times it: 50 distinct sliding layers (L 786,
     W 1024) captured in one HIP graph.  Every replay equals the eager calls
-    bit for bit (eager work and synchronisations between replays), and the
-    layers match the oracle."""
+    bit for bit (eager work on the same workspace and synchronisations
+    between replays), and the layers match the oracle."""
     Hq, Hkv, D, L, W, layers = 32, 16, 256, 786, 1024, 50
     g = torch.Generator(device="cuda").manual_seed(786)
     sets = [gpu_cache(gpu, Hkv, L, D, g) for _ in range(layers)]
@@ -106,11 +106,16 @@ def test_sliding50_graph_step(gpu):
         for s, o in zip(sets, outs):
             gpu.sdpa_int4(qd, *s, Hq // Hkv, 1.0, W, out=o)
 
-    step()
+    # The eager calls run on the capture stream, so the graph's kernels and
+    # the eager calls between replays use that stream's one workspace (it
+    # exists before capture, so nothing is allocated while capturing).
+    cs = torch.cuda.Stream()
+    with torch.cuda.stream(cs):
+        step()
     torch.cuda.synchronize()
     eager = [host(o).copy() for o in outs]
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=cs):
         step()
     for rep in range(3):
         for o in outs:
@@ -119,8 +124,9 @@ def test_sliding50_graph_step(gpu):
         torch.cuda.synchronize()
         for i, o in enumerate(outs):
             assert np.array_equal(host(o), eager[i]), f"replay {rep} layer {i}"
-        # eager work on the same workspace between replays
-        gpu.sdpa_int4(qd, *sets[rep], Hq // Hkv, 1.0, W, out=outs[0])
+        # eager work on the graph's workspace between replays
+        with torch.cuda.stream(cs):
+            gpu.sdpa_int4(qd, *sets[rep], Hq // Hkv, 1.0, W, out=outs[0])
         torch.cuda.synchronize()
     for i in (0, 17, 49):
         ref = O.sdpa_int4(qv, *[host(t) for t in sets[i]], Hq // Hkv, 1.0, W)
@@ -149,11 +155,13 @@ def test_mixed_layers_graph_step(gpu):
         gpu.sdpa_int4(qg, *glob, 8, 1.0, 0, out=outg)
         gpu.sdpa_int4(qs, *slid[2], 2, 1.0, 1024, out=outs[2])
 
-    step()
+    cs = torch.cuda.Stream()  # eager calls and capture share this stream's workspace
+    with torch.cuda.stream(cs):
+        step()
     torch.cuda.synchronize()
     eager = [host(o).copy() for o in outs + [outg]]
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=cs):
         step()
     for rep in range(3):
         for o in outs + [outg]:
@@ -162,8 +170,9 @@ def test_mixed_layers_graph_step(gpu):
         torch.cuda.synchronize()
         for i, o in enumerate(outs + [outg]):
             assert np.array_equal(host(o), eager[i]), f"replay {rep} output {i}"
-        # eager work on the same workspace between replays
-        gpu.sdpa_int4(qg, *glob, 8, 1.0, 0, out=outg)
+        # eager work on the graph's workspace between replays
+        with torch.cuda.stream(cs):
+            gpu.sdpa_int4(qg, *glob, 8, 1.0, 0, out=outg)
         torch.cuda.synchronize()
     check_heads(eager[3], qgv, glob, (1,), 8, what="global layer in the graph")
 

@@ -68,8 +68,13 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(tq_env):
     """A shape whose split-K workspace exceeds the static 8 MiB is refused
     on the host, before any device call (so this runs without a GPU)."""
     tq_env("TQ_SDPA_CHUNK", "128")  # 256 splits: 32 heads x 256 x 1 KiB of partials
+    lib = _lib.load()
+    assert lib.tq_sdpa_int4_workspace_size(1, 32, 16, 256, 32768) > 8 << 20
+    # Fake pointers, and a k_quant that is not 16-byte aligned: whichever
+    # host check runs first refuses the call, so no kernel ever sees them.
     f = ctypes.c_void_p(0x10000)
-    st = _lib.load().tq_sdpa_int4_noalloc(f, _lib.TQ_BF16, f, f, f, f, f, f, _lib.TQ_F16, f, 32,
-                                          16, 256, 32768, 32768, 2, 1.0, 0, None)
+    kq = ctypes.c_void_p(0x10008)
+    st = lib.tq_sdpa_int4_noalloc(f, _lib.TQ_BF16, kq, f, f, f, f, f, _lib.TQ_F16, f, 32,
+                                  16, 256, 32768, 32768, 2, 1.0, 0, None)
     assert st == 2  # TQ_ERR_UNSUPPORTED
     assert "scratch" in _lib.last_error()
