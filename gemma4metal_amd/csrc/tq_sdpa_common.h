@@ -257,6 +257,16 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A split's (m, l) pair as one 8-byte access (p 8-byte aligned).
+__device__ __forceinline__ void store_coherent_pair(float* p, float m, float l) {
+  const uint64_t v = static_cast<uint64_t>(__float_as_uint(m)) | (static_cast<uint64_t>(__float_as_uint(l)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_coherent_pair(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return float2{__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32))};
+}
 
 __device__ __forceinline__ float normalise(float O, float L, float eps) {
   return eps > 0.0f ? O / (L + eps) : (L > 0.0f ? O / L : 0.0f);
@@ -333,33 +343,46 @@ struct Finalize {
   // arena (no barrier needed before the call).  Column h is output row
   // head_base + (h / gh) * qstride + h % gh (decode: head_base = b*Hq + first
   // head, rows head_base + h); columns h >= nvalid are dropped.
+  //
+  // Both merges here (the NW per-wave partials of this workgroup, then the S
+  // split partials in the last workgroup) weight partial k by
+  // f_k = 2^(m_k - M), M = max m_k.  A wave's 64 outputs share one head (64
+  // divides D), so the weights are wave-uniform: lane k computes f_k (one
+  // exp2 per lane, not one per output and partial), the denominator is a
+  // lane reduction, and each output then takes one FMA per partial with f_k
+  // read back as a scalar.
   __device__ static void run(const SdpaParams& p, float* arena, int64_t head_base, int S,
                              int split, int counter, int gh = G, int64_t qstride = 0,
                              int nvalid = G) {
+    static_assert(D % 64 == 0, "one head per wave");
+    static_assert(NW <= 16, "per-wave partials fit one row of 16 lanes");
+    constexpr int NI = (G * D + kNT - 1) / kNT;  // outputs per thread
     auto row = [&](int h) -> int64_t { return head_base + (h / gh) * qstride + h % gh; };
+    const int lane = threadIdx.x & 63;
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int idx = threadIdx.x + i * kNT;
       const int h = idx / D, d = idx - (idx / D) * D;
-      if (h >= nvalid) continue;
-      float M = -INFINITY;
+      if (idx >= G * D || h >= nvalid) continue;  // wave-uniform
+      // lane w < NW: wave w's (m, l) of head h (each row of 16 lanes holds
+      // the same copy, so a row reduction is the workgroup's)
+      const int w = lane & 15;
+      const float mw = w < NW ? m(arena, w)[h] : -INFINITY;
+      const float lw = w < NW ? l(arena, w)[h] : 0.0f;
+      const float M = row16_max(mw);
+      const float fw = merge_factor(mw, M);
+      const float Ls = group_sum<16>(lw * fw);
+      float O = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) M = fmaxf(M, m(arena, w)[h]);
-      float O = 0.0f, Ls = 0.0f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float f = merge_factor(m(arena, w)[h], M);
-        O += o(arena, w, h)[d] * f;
-        Ls += l(arena, w)[h] * f;
-      }
+      for (int k = 0; k < NW; ++k)
+        O = fmaf(o(arena, k, h)[d], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fw), k)), O);
       if (S == 1) {
         p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
       } else {
         const int64_t slot = row(h) * p.max_splits + split;
         store_coherent(p.ws_o + slot * D + d, O);
-        if (d == 0) {
-          store_coherent(p.ws_ml + slot * 2, M);
-          store_coherent(p.ws_ml + slot * 2 + 1, Ls);
-        }
+        if (d == 0) store_coherent_pair(p.ws_ml + slot * 2, M, Ls);
       }
     }
     if (S == 1 || p.ext_merge) return;
@@ -391,47 +414,52 @@ struct Finalize {
     __syncthreads();
     if (!s_last) return;
 
-    // Each thread merges its (head, dim) outputs, KC splits at a time.  A
-    // wave's outputs share one head (64 divides D), so lane k loads split
-    // s0 + k's (m, l) and v_readlane hands them to the whole wave; those two
-    // loads and the KC partial loads (coalesced over dims) all go out before
-    // the first use: one memory round trip per chunk, one in all for S <= KC.
+    // Merge, KC splits at a time: lane k (mod 16) loads split s0 + k's
+    // (m, l), and every lane the KC partials of its outputs (coalesced over
+    // dims).  All loads of a chunk, for all of a thread's outputs, go out
+    // before the first use: one memory round trip per chunk, one in all for
+    // S <= KC.
     constexpr int KC = 16;
-    static_assert(D % 64 == 0, "one head per wave");
-    const int lane = threadIdx.x & 63;
-    for (int idx = threadIdx.x; idx < G * D; idx += kNT) {
-      const int h = idx / D, d = idx - (idx / D) * D;
-      if (h >= nvalid) continue;  // wave-uniform
-      const float* ml = p.ws_ml + row(h) * p.max_splits * 2;
-      const float* po = p.ws_o + row(h) * p.max_splits * D + d;
-      float M = -INFINITY, Ls = 0.0f, O = 0.0f;
-      for (int s0 = 0; s0 < S; s0 += KC) {
-        const int sl = min(s0 + (lane & (KC - 1)), S - 1);
-        const float mv = load_coherent(ml + 2 * sl);
-        const float lv = load_coherent(ml + 2 * sl + 1);
-        float ok[KC];
+    float Mr[NI], Lr[NI], Or[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) { Mr[i] = -INFINITY; Lr[i] = 0.0f; Or[i] = 0.0f; }
+    for (int s0 = 0; s0 < S; s0 += KC) {
+      float2 mlv[NI];
+      float ok[NI][KC];
+      const int sl = min(s0 + (lane & (KC - 1)), S - 1);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int idx = threadIdx.x + i * kNT;
+        // (past the last output: a valid row, loaded and dropped below)
+        const int h = min(idx / D, nvalid - 1), d = idx - (idx / D) * D;
+        mlv[i] = load_coherent_pair(p.ws_ml + (row(h) * p.max_splits + sl) * 2);
+        const float* po = p.ws_o + row(h) * p.max_splits * D + d;
 #pragma unroll
         for (int k = 0; k < KC; ++k)
-          ok[k] = load_coherent(po + static_cast<int64_t>(min(s0 + k, S - 1)) * D);
-        float mk[KC], Mn = M;
-#pragma unroll
-        for (int k = 0; k < KC; ++k) {
-          mk[k] = s0 + k < S ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mv), k))
-                             : -INFINITY;
-          Mn = fmaxf(Mn, mk[k]);
-        }
-        const float fr = merge_factor(M, Mn);
-        Ls *= fr;
-        O *= fr;
-#pragma unroll
-        for (int k = 0; k < KC; ++k) {
-          const float f = merge_factor(mk[k], Mn);
-          Ls = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv), k)), f, Ls);
-          O = fmaf(ok[k], f, O);
-        }
-        M = Mn;
+          ok[i][k] = load_coherent(po + static_cast<int64_t>(min(s0 + k, S - 1)) * D);
       }
-      p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        // lanes past the splits get m = -inf, hence weight 0
+        const float mk = s0 + (lane & (KC - 1)) < S ? mlv[i].x : -INFINITY;
+        const float Mn = fmaxf(Mr[i], row16_max(mk));
+        const float fr = merge_factor(Mr[i], Mn);
+        const float fk = merge_factor(mk, Mn);
+        Lr[i] = fmaf(Lr[i], fr, group_sum<16>(mlv[i].y * fk));
+        float O = Or[i] * fr;
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+          O = fmaf(ok[i][k], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fk), k)), O);
+        Or[i] = O;
+        Mr[i] = Mn;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int idx = threadIdx.x + i * kNT;
+      const int h = idx / D, d = idx - (idx / D) * D;
+      if (idx >= G * D || h >= nvalid) continue;
+      p.out[row(h) * D + d] = normalise(Or[i], Lr[i], p.denom_eps);
     }
   }
 };
