@@ -322,20 +322,27 @@ __device__ __forceinline__ void pace_waves(int* done_lds, int wv, int lane, int 
   }
 }
 
-// LDS arena of the finalisation: [o: NW*G*D | m: NW*G | l: NW*G] (sized to
-// at least 2*G*kMaxSplits floats, room for per-split (m, l) pairs).  NW =
+// LDS arena of the finalisation: [o: NW*SPW*G*D | m: NW*G | l: NW*G |
+// corr: NW*SPW*G*(D/64)] (sized to at least 2*G*kMaxSplits floats).  NW =
 // partial results per workgroup (one per wave, or per key stream), NT =
-// threads.
-template <int G, int D, int NW = kWaves, int NT = NW * 64>
+// threads.  A wave may leave its partial O as SPW rows per head (slots
+// SPW*w .. SPW*w + SPW - 1, summed here) and, with CORR, one additive term
+// per slot and (head, quant group) that applies to every dim of the group
+// (the matrix-core kernel's hi and lo weight parts and their corrections).
+template <int G, int D, int NW = kWaves, int NT = NW * 64, int SPW = 1, bool CORR = false>
 struct Finalize {
   static constexpr int kNT = NT;
-  static constexpr int kArena = (NW * G * D + 2 * NW * G) > (2 * G * kMaxSplits)
-                                    ? (NW * G * D + 2 * NW * G)
-                                    : (2 * G * kMaxSplits);
-  __device__ static float* o(float* arena, int w, int h) { return arena + (w * G + h) * D; }
-  __device__ static float* m(float* arena, int w) { return arena + NW * G * D + w * G; }
+  static constexpr int NGc = D / 64;
+  static constexpr int kUsed = NW * SPW * G * D + 2 * NW * G + (CORR ? NW * SPW * G * NGc : 0);
+  static constexpr int kArena = kUsed > 2 * G * kMaxSplits ? kUsed : 2 * G * kMaxSplits;
+  __device__ static float* o(float* arena, int slot, int h) { return arena + (slot * G + h) * D; }
+  __device__ static float* m(float* arena, int w) { return arena + NW * SPW * G * D + w * G; }
   __device__ static float* l(float* arena, int w) {
-    return arena + NW * G * D + NW * G + w * G;
+    return arena + NW * SPW * G * D + NW * G + w * G;
+  }
+  // [h * (D / 64) + group] of a slot
+  __device__ static float* corr(float* arena, int slot) {
+    return arena + NW * SPW * G * D + 2 * NW * G + slot * G * NGc;
   }
 
   // Called by all threads after every wave stored its unnormalised output
@@ -374,9 +381,21 @@ struct Finalize {
       const float fw = merge_factor(mw, M);
       const float Ls = group_sum<16>(lw * fw);
       float O = 0.0f;
+      if constexpr (CORR) {
+        // the corrections of this wave's group (d / 64 is wave-uniform)
+        float cw = 0.0f;
+        if (w < NW) {
 #pragma unroll
-      for (int k = 0; k < NW; ++k)
-        O = fmaf(o(arena, k, h)[d], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fw), k)), O);
+          for (int t = 0; t < SPW; ++t) cw += corr(arena, w * SPW + t)[h * NGc + d / 64];
+        }
+        O = group_sum<16>(cw * fw);
+      }
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+        const float fk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fw), k));
+#pragma unroll
+        for (int t = 0; t < SPW; ++t) O = fmaf(o(arena, k * SPW + t, h)[d], fk, O);
+      }
       if (S == 1) {
         p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
       } else {

@@ -240,9 +240,12 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   const int col_hi = pos;
   const int col_lo = p.window > 0 ? pos - p.window + 1 : 0;
 
-  // One partial result per wave (with packed columns the hi- and lo-part
-  // columns' products are summed in registers first).
-  using Fin = Finalize<G, D, NW, NW * 64>;
+  // One partial result per wave; with packed columns a wave leaves its hi-
+  // and lo-part rows and their corrections as two slots, which the
+  // workgroup combine sums (a lane holds 64 values of one column part; a
+  // cross-lane sum and a correction per value in every wave would cost
+  // ~200 instructions on the workgroup's critical path).
+  using Fin = Finalize<G, D, NW, NW * 64, PACK ? 2 : 1, PACK>;
   __shared__ __align__(16) float arena[Fin::kArena];
   // scales staged per wave as [array][group][key pair] fp16x2, or
   // [array][group][key] fp32
@@ -695,7 +698,8 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     bacc += ror8(bacc);
     if (T) bacc = 0.0f;  // counted once, in the hi part
   }
-  const int slot = wave;
+  // packed: slot 2 * wave + T holds column n's part T (hi / lo)
+  const int slot = PACK ? 2 * wave + T : wave;
   const float corr = bacc - 128.0f * wsum;  // bias term and the 128 offset
   if (col_used) {
     // Accumulator element (s, j) of C row 4c + i is dim 8 * (VW * (4c + i) +
@@ -703,7 +707,8 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     // quant group, so a lane writes the rows of its column's group as whole
     // vectors.  A wave's arena slot covers every dim: its own V words' dims
     // get the result, the other V half's dims zero; only V half 0 counts the
-    // denominator (both halves scored the same keys).
+    // denominator (both halves scored the same keys).  Packed columns write
+    // raw rows, and the correction once per (slot, column).
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int dim0 = 8 * VW * (4 * c + i);
@@ -717,23 +722,21 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
             float v = 0.0f;
 #pragma unroll
             for (int s2 = 0; s2 < VWH; ++s2)
-              if (s2 == so) v = cv[8 * s2 + j][i] + corr;
-            // packed: lane m + 8 holds the lo part of lane m's column (the
-            // pair agrees on every branch here)
-            if constexpr (PACK) v += ror8(v);
+              if (s2 == so) v = PACK ? cv[8 * s2 + j][i] : cv[8 * s2 + j][i] + corr;
             row[8 * sg + j] = v;
           }
         v4f* dst = reinterpret_cast<v4f*>(Fin::o(arena, slot, hn) + dim0);
-        if (T == 0) {
 #pragma unroll
-          for (int q4 = 0; q4 < 2 * VW; ++q4)
-            dst[q4] = v4f{row[4 * q4], row[4 * q4 + 1], row[4 * q4 + 2], row[4 * q4 + 3]};
-        }
+        for (int q4 = 0; q4 < 2 * VW; ++q4)
+          dst[q4] = v4f{row[4 * q4], row[4 * q4 + 1], row[4 * q4 + 2], row[4 * q4 + 3]};
       }
     }
+    if constexpr (PACK) {
+      if (c == 0) Fin::corr(arena, slot)[n] = corr;
+    }
     if (gn == 0 && c == 0 && T == 0) {
-      Fin::m(arena, slot)[hn] = m_run;
-      Fin::l(arena, slot)[hn] = vhalf == 0 ? l_sum : 0.0f;
+      Fin::m(arena, wave)[hn] = m_run;
+      Fin::l(arena, wave)[hn] = vhalf == 0 ? l_sum : 0.0f;
     }
   }
   if constexpr (kQG)
