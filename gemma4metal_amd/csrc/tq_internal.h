@@ -142,6 +142,29 @@ __device__ __forceinline__ float row16_max(float v) {
   return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
 }
 
+// Max over aligned groups of N consecutive lanes (N = 16, 32 or 64), every
+// lane of the group receiving it.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(N == 16 || N == 32 || N == 64, "N");
+  v = row16_max(v);
+  if constexpr (N >= 32) v = xor16_max(v);
+  if constexpr (N >= 64) v = xor32_max(v);
+  return v;
+}
+
+// Exact int32 sum over aligned groups of N consecutive lanes (N <= 16), the
+// butterfly of group_sum.
+template <int N>
+__device__ __forceinline__ int group_sum_i(int v) {
+  static_assert(N == 2 || N == 4 || N == 8 || N == 16, "N");
+  if constexpr (N >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  if constexpr (N >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  if constexpr (N >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  if constexpr (N >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  return v;
+}
+
 // The same butterfly over all 64 lanes for a max, and for an exact int32
 // sum: four DPP steps inside each row of 16 lanes, then the two cross-row
 // permlane swaps.

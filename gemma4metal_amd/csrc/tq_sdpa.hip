@@ -518,6 +518,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   TQ_CHECK_ARG(q && kq && ks && kb && vq && vs && vb && out, "%s: null tensor pointer", fn);
   TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(kq) % 16 == 0 && reinterpret_cast<uintptr_t>(vq) % 16 == 0,
                "%s: k_quant / v_quant must be 16-byte aligned", fn);
+  TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(q) % 16 == 0, "%s: queries must be 16-byte aligned", fn);
   TQ_CHECK_ARG(std::isfinite(scale), "%s: scale must be finite", fn);
 
   const int mode = prefill ? 2 : (seq_lens ? 1 : 0);

@@ -194,7 +194,14 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   constexpr int SKP = F32 ? 32 : 16;     // staged scale slots per (array, group)
   constexpr int NWK = NW / VS;       // waves per key stream
   constexpr int RW = D / 8;
-  constexpr int NE = (G * D + kNT - 1) / kNT;  // q elements per thread
+  // K.q B image: word (k, i, n, ccl) = ((k * KM + i) * QCOL + n) * QCC + ccl
+  // holds the 16 k-slots of digit k, MFMA i, column n, for the ccl-th lane
+  // group whose dims lie in column n's quant group (D 128: lane groups 2g,
+  // 2g + 1; D 256: g; D 512: g / 2, zero for the MFMAs of the other group).
+  constexpr int QCOL = PACK ? 8 : 16;
+  constexpr int QCC = D == 128 ? 2 : 1;
+  constexpr int QWORDS = 3 * KM * QCOL * QCC;
+  constexpr int NCH = (G * D + 511) / 512;  // 8-element q chunks per lane
 
   pin_args(p);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -250,11 +257,13 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // scales staged per wave as [array][group][key pair] fp16x2, or
   // [array][group][key] fp32
   __shared__ __align__(16) uint32_t sc_lds[NW][4][NG][SKP];
-  __shared__ uint4 bk_lds[NTB][3][KM][64];       // B operands of the K MFMAs
-  __shared__ float red_max[NE][NW];
-  __shared__ float sh_qhat[G][NG];
-  __shared__ int sh_F[G];
-  __shared__ int s_done[NW];  // iterations processed, per wave (issue pacing)
+  // B operands of the K MFMAs: one compact image per wave (built by the wave
+  // itself, see the prologue), and one all-zero image of the same layout
+  // ([NW]) that lanes read where their column has no digits.
+  __shared__ __align__(16) uint4 qimg[NW + 1][QWORDS];
+  // iterations processed, per wave (issue pacing; each wave zeroes its own
+  // entry, and a partner's read before that only sets an issue priority)
+  __shared__ int s_done[NW];
   if ((threadIdx.x & 63) == 0) s_done[threadIdx.x >> 6] = 0;
 
   // ---- first loads, issued before the prologue to overlap its latency ------
@@ -285,25 +294,24 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   // capacities of at least 32 rows.  Wave-uniform (scalar).
   auto block_row = [&](int t0) { return max(0, min(t0, t_end - 32)); };
 
-  // q is loaded first: at kernel start every workgroup issues its K/V stream
-  // at once, and the prologue (which needs only q) should not wait for it.
-  // Then the first iteration's K/V loads go out and stay in flight while
-  // the prologue runs.
-  // (one dword load per element for every q dtype -- no branch around the
-  // load, so the wait before the prologue covers q only, not the K/V loads
-  // issued after it)
-  uint32_t qraw[NE], qsh[NE];  // dword of each element, and its 16-bit half
-  const int qsz = p.q_dtype == TQ_F32 ? 4 : 2;
+  // q is loaded first, then the first block's K/V, which stay in flight
+  // while the prologue runs.  Every wave loads all G * D q elements of its
+  // column sets (8 per lane and chunk: one or two 16-byte loads, the same
+  // two loads for every dtype, so no branch separates them from the K/V
+  // loads and the prologue's wait covers q only).
+  uint4 qa[NCH], qb[NCH];
+  const bool q32 = p.q_dtype == TQ_F32;
 #pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    // element e of column set v = e / D: query min(b0 + v / GH, b_last),
-    // head h0 + v % GH
-    const int e = min(static_cast<int>(threadIdx.x) + k * kNT, G * D - 1);
-    const int v = e / D;
+  for (int s = 0; s < NCH; ++s) {
+    // chunk ch: elements 8 ch .. 8 ch + 7 of column set v = 8 ch / D, i.e.
+    // query min(b0 + v / GH, b_last), head h0 + v % GH (clamped chunks are
+    // dropped below)
+    const int ch = min(lane + 64 * s, G * D / 8 - 1);
+    const int v = 8 * ch / D;
     const int64_t qrow = static_cast<int64_t>(min(b0 + v / GH, b_last)) * p.Hq + h0 + v % GH;
-    const int64_t byte = (qrow * D + (e - v * D)) * qsz;
-    qraw[k] = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p.q) + (byte & ~int64_t{3}));
-    qsh[k] = qsz == 2 && (byte & 2) ? 16u : 0u;  // applied at conversion, not here
+    const char* qp = static_cast<const char*>(p.q) + (qrow * D + (8 * ch - v * D)) * (q32 ? 4 : 2);
+    qa[s] = *reinterpret_cast<const uint4*>(qp);
+    qb[s] = *reinterpret_cast<const uint4*>(qp + (q32 ? 16 : 0));
   }
   __builtin_amdgcn_sched_barrier(0);
   // Issued unconditionally (a load under a branch makes the compiler drain
@@ -313,75 +321,110 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   load_iter<D, G, F32, kStreamNT>(bufA, kq_row0, vq_row0, sc_arr, lo, block_row(base0));
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- prologue: q as 22-bit fixed point per head, B operands via LDS ------
-  float qv[NE];
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const uint32_t w = qraw[k] >> qsh[k];
-    const float f = p.q_dtype == TQ_F32 ? __uint_as_float(w)
-                    : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(w & 0xFFFFu)))
-                                          : __uint_as_float(w << 16);
-    qv[k] = threadIdx.x + k * kNT < G * D ? f * p.scale_log2 : 0.0f;
-  }
-#pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const float mx = wave_max_dpp(fabsf(qv[k]));
-    if (lane == 0) red_max[k][wave] = mx;
-  }
+  // ---- prologue: q as 22-bit fixed point per column set, B image per wave ---
+  // Each wave builds the whole image it reads, so no barrier orders the
+  // prologue: a wave starts its stream as soon as its own q has arrived.
+  // The digits equal those of one image shared by the workgroup (the
+  // exponent F is the column set's, from its maximum over all D dims).
   {
-    uint4* z = &bk_lds[0][0][0][0];
-    for (int i = threadIdx.x; i < NTB * 3 * KM * 64; i += kNT) z[i] = uint4{0u, 0u, 0u, 0u};
+    uint4* zi = &qimg[wv][0];
+    uint4* zz = &qimg[NW][0];  // every wave writes the same zeros here
+#pragma unroll
+    for (int i = lane; i < QWORDS; i += 64) {
+      zi[i] = uint4{0u, 0u, 0u, 0u};
+      zz[i] = uint4{0u, 0u, 0u, 0u};
+    }
   }
-  __syncthreads();
-  // Every wave slot (k, w) holds 64 consecutive elements: one quant group of
-  // one head, since 64 | D and 64 | kNT.
-  uint8_t* bk_bytes = reinterpret_cast<uint8_t*>(&bk_lds[0][0][0][0]);
+  int Fs[NCH];
+  float qhs[NCH];
 #pragma unroll
-  for (int k = 0; k < NE; ++k) {
-    const int e0 = wave * 64 + k * kNT;  // first element of this wave slot
-    if (e0 < G * D) {                          // wave-uniform
-      const int h = e0 / D;
-      float hm = 0.0f;
+  for (int s = 0; s < NCH; ++s) {
+    const int ch = lane + 64 * s;
+    const bool ok = ch < G * D / 8;
+    float f[8];
+    const uint32_t w16[4] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w};
+    const uint32_t w32[8] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w, qb[s].x, qb[s].y, qb[s].z, qb[s].w};
 #pragma unroll
-      for (int k2 = 0; k2 < NE; ++k2)
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h16 = (w16[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      const float x = q32 ? __uint_as_float(w32[e])
+                      : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(h16)))
+                                            : __uint_as_float(h16 << 16);
+      f[e] = ok ? x * p.scale_log2 : 0.0f;
+    }
+    float amax = 0.0f;
 #pragma unroll
-        for (int w2 = 0; w2 < NW; ++w2) {
-          const int f0 = w2 * 64 + k2 * kNT;
-          if (f0 < G * D && f0 / D == h) hm = fmaxf(hm, red_max[k2][w2]);
-        }
-      int ex = 0;
-      if (hm > 0.0f) frexpf(hm, &ex);  // hm < 2^ex
-      const int F = 22 - ex;           // |round(q * 2^F)| <= 2^22
-      const int X = static_cast<int>(__builtin_rintf(qv[k] * ldexpf(1.0f, F)));
-      const int d = (e0 - h * D) + lane;
-      // scatter the three base-256 digits into the B image of lane (16c + n)
-      const int nn = h * NG + (d >> 6), cc = d / (D / 4), off = d % (D / 4);
-      const int i = off >> 4, r16 = off & 15, nib = r16 & 7;
-      const int v = 2 * (r16 >> 3) + (nib & 1), by = nib >> 1;
-      const int byte0 = ((i * 64 + 16 * cc + nn) * 16) + v * 4 + by;
-      const int d0 = static_cast<int8_t>(X & 0xFF);
-      const int X1 = (X - d0) >> 8;
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+    // the column set's D / 8 chunks are D / 8 consecutive lanes of one slot
+    amax = group_max<(D / 8 < 64 ? D / 8 : 64)>(amax);
+    int ex = 0;
+    if (amax > 0.0f) frexpf(amax, &ex);  // amax < 2^ex
+    const int F = 22 - ex;               // |round(q * 2^F)| <= 2^22
+    const float sF = ldexpf(1.0f, F);
+    int X[8], xs = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      X[e] = static_cast<int>(__builtin_rintf(f[e] * sF));
+      xs += X[e];
+    }
+    // sum over the quant group's 64 dims (8 lanes), exact: 64 * 2^22 < 2^31
+    xs = group_sum_i<8>(xs);
+    Fs[s] = F;
+    qhs[s] = static_cast<float>(xs) * ldexpf(1.0f, -F);
+    // three signed base-256 digits per element; bytes of elements 0, 2, 4, 6
+    // (even) and 1, 3, 5, 7 (odd) form two dwords of the 16 k-slots of
+    // this chunk's MFMA, lane group and column
+    uint32_t ev[3] = {0u, 0u, 0u}, od[3] = {0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d0 = static_cast<int8_t>(X[e] & 0xFF);
+      const int X1 = (X[e] - d0) >> 8;
       const int d1 = static_cast<int8_t>(X1 & 0xFF);
       const int d2 = (X1 - d1) >> 8;
-      bk_bytes[byte0] = static_cast<uint8_t>(d0);
-      bk_bytes[byte0 + KM * 64 * 16] = static_cast<uint8_t>(d1);
-      bk_bytes[byte0 + 2 * KM * 64 * 16] = static_cast<uint8_t>(d2);
-      if constexpr (PACK) {  // tile 1's image: the same digits in column nn + 8
-        const int byte1 = byte0 + 3 * KM * 64 * 16 + 8 * 16;
-        bk_bytes[byte1] = static_cast<uint8_t>(d0);
-        bk_bytes[byte1 + KM * 64 * 16] = static_cast<uint8_t>(d1);
-        bk_bytes[byte1 + 2 * KM * 64 * 16] = static_cast<uint8_t>(d2);
-      }
-      const int gsum = wave_sum_dpp(X);  // exact: 64 * 2^22 < 2^31
-      if (lane == 0) {
-        sh_qhat[h][d >> 6] = static_cast<float>(gsum) * ldexpf(1.0f, -F);
-        if ((d >> 6) == 0) sh_F[h] = F;
+      const int sh = 8 * (e >> 1);
+      uint32_t* dst = (e & 1) ? od : ev;
+      dst[0] |= static_cast<uint32_t>(d0 & 0xFF) << sh;
+      dst[1] |= static_cast<uint32_t>(d1 & 0xFF) << sh;
+      dst[2] |= static_cast<uint32_t>(d2 & 0xFF) << sh;
+    }
+    if (ok) {
+      const int v = 8 * ch / D, dim0 = 8 * ch - v * D;
+      const int nn = v * NG + dim0 / 64;                       // column
+      const int cc = dim0 / (D / 4), off = dim0 - cc * (D / 4);  // lane group, k-slot offset
+      const int i = off >> 4, half = (off >> 3) & 1;
+      char* w0 = reinterpret_cast<char*>(&qimg[wv][(i * QCOL + nn) * QCC + cc % QCC]) + 8 * half;
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        *reinterpret_cast<uint2*>(w0 + k * (KM * QCOL * QCC * 16)) = uint2{ev[k], od[k]};
+    }
+  }
+  // this lane's column: its set's exponent and the group's sum of q, from the
+  // lane holding the group's first chunk
+  float sf = 0.0f, qhat = 0.0f;
+  {
+    const int chn = col_used ? (hn * D + 64 * gn) / 8 : 0;
+#pragma unroll
+    for (int s = 0; s < NCH; ++s) {
+      const int Fv = __shfl(Fs[s], chn & 63, 64);
+      const float qv = __shfl(qhs[s], chn & 63, 64);
+      if ((chn >> 6) == s && col_used) {
+        sf = ldexpf(1.0f, -Fv);
+        qhat = qv;
       }
     }
   }
-  __syncthreads();
-  const float sf = col_used ? ldexpf(1.0f, -sh_F[hn]) : 0.0f;
-  const float qhat = col_used ? sh_qhat[hn][gn] : 0.0f;
+  // B operand addresses of this lane, per key tile: its wave's image where
+  // its (column, lane group) pair carries digits, else the zero image
+  const uint4* bq_addr[NTB];
+  {
+    const bool grp = D == 128 ? (c >> 1) == gn : (D == 256 ? c == gn : c == (gn >> 1));
+    const int wofs = n * QCC + (D == 128 ? (c & 1) : 0);
+#pragma unroll
+    for (int t = 0; t < NTB; ++t) {
+      const bool has = col_used && grp && (!PACK || T == t);
+      bq_addr[t] = &qimg[has ? wv : NW][wofs];
+    }
+  }
 
   // ---- main loop ----------------------------------------------------------
   float m_run = -INFINITY, l_run = 0.0f, wsum = 0.0f, bacc = 0.0f;
@@ -466,7 +509,7 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
         for (int k = 0; k < 3; ++k) {
           // B operands live in LDS (16 B per lane per MFMA) to keep the wave
           // within 256 registers
-          const uint4 u = bk_lds[img][k][i][lane];
+          const uint4 u = bq_addr[img][(k * KM + i) * QCOL * QCC];
           const v4i bq = v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z),
                              static_cast<int>(u.w)};
           acc[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, acc[k], 0, 0, 0);

@@ -74,7 +74,8 @@ int tq_stream_read_tiles(const void* src, size_t bytes, uint32_t* sink, int bloc
  * the dequantized rows of kv head h / gqa_factor; key ki is skipped when
  * sliding_window > 0 and kv_len-1-ki >= sliding_window
  * (lib/turboquant.metal:779); an empty key set gives 0 (:886).
- *   q        [num_heads, head_dim] in q_dtype (f32, f16 or bf16)
+ *   q        [num_heads, head_dim] in q_dtype (f32, f16 or bf16), 16-byte
+ *            aligned (as k_quant and v_quant)
  *   out      [num_heads, head_dim] f32
  *   head_dim in {128, 256, 512}; num_heads == num_kv_heads * gqa_factor
  *   kv_capacity >= kv_len is the row stride of each head (== kv_len for a
