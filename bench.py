@@ -110,6 +110,21 @@ def prewarm(torch, fn, seconds=PREWARM_S):
         torch.cuda.synchronize()
 
 
+# Rotated input sets must exceed the 256 MB Infinity Cache (MALL) by a
+# margin, or repeats are served from it: at least 512 MiB of distinct KV per
+# timed workload, at most 2 GiB.
+MALL_PROOF_BYTES = 512 << 20
+
+
+def rotation_sets(wanted, set_bytes):
+    """Number of distinct input sets to rotate: at least `wanted` and at
+    least 512 MiB in all (so the MALL cannot serve a repeat), at most 2 GiB
+    in all, and never fewer than 2."""
+    need = -(-MALL_PROOF_BYTES // max(1, set_bytes))
+    cap = (2 << 30) // max(1, set_bytes)
+    return max(2, min(max(wanted, need), cap))
+
+
 def time_launches(torch, fn, steps, warmup):
     """(whole-region ms per step, mean per-launch ms) with HIP events on the
     current stream -- the stream every launch is issued on.  A time-based
@@ -181,7 +196,7 @@ def main():
         lines = []
         for L in lens:
             row = O.row_bytes(D, sb_bytes)
-            nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkv * L * row)))
+            nsets = rotation_sets(args.sets, Hkv * L * row)
             sets = [gen_cache(tq, torch, Hkv, L, D, gen, sb=sbt) for _ in range(nsets)]
             qs = [gen_q(torch, (Hq, D), gen) for _ in range(nsets)]
             out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
@@ -203,7 +218,8 @@ def main():
                 "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                 "dtype": precision_note(args.sb),
                 "data": "synthetic (seeded N(0,1), RMS-normed Q/K), random-init; "
-                        f"{nsets} rotated KV sets",
+                        f"{nsets} rotated KV sets ({nsets * Hkv * L * row / 2**20:.0f} MiB, more "
+                        "than the 256 MB MALL)",
                 "config": {"workload": f"sdpa_int4 decode layer Hq={Hq} Hkv={Hkv} D={D} "
                                        f"L={L} W=0, {args.sb} scale/bias (BASELINE configs[2])",
                            "global_batch": 1, "seq_len": L, "parallelism": "none (1 GPU)"},
@@ -284,7 +300,7 @@ def main():
         # Gemma global-attention layer shape (engine/gemma4_multilayer.cpp:3,49-51):
         # Hq 32, Hkv 4 (GQA 8), D 512, no window
         Hg, Hkvg, Dg, L = 32, 4, 512, args.ctx
-        nsets = max(2, min(args.sets, (2 << 30) // max(1, Hkvg * L * O.row_bytes(Dg, sb_bytes))))
+        nsets = rotation_sets(args.sets, Hkvg * L * O.row_bytes(Dg, sb_bytes))
         sets = [gen_cache(tq, torch, Hkvg, L, Dg, gen, sb=sbt) for _ in range(nsets)]
         qs = [gen_q(torch, (Hg, Dg), gen) for _ in range(nsets)]
         out = torch.empty((Hg, Dg), dtype=torch.float32, device="cuda")
@@ -307,24 +323,33 @@ def main():
 
     if args.workload == "sliding50":
         L, W, layers = 786, 1024, 50
-        sets = [gen_cache(tq, torch, Hkv, L, D, gen, sb=sbt) for _ in range(layers)]
+        # distinct 50-layer steps (one HIP graph each), rotated so that the
+        # KV read by consecutive steps exceeds the MALL
+        layer_bytes = Hkv * L * O.row_bytes(D, sb_bytes)
+        nsteps = rotation_sets(1, layers * layer_bytes)
+        steps_kv = [[gen_cache(tq, torch, Hkv, L, D, gen, sb=sbt) for _ in range(layers)]
+                    for _ in range(nsteps)]
         q = gen_q(torch, (Hq, D), gen)
         out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
         nbytes = O.decode_bytes(Hq, Hkv, D, L, sb_bytes=sb_bytes)
 
-        def one_step():
+        def one_step(sets):
             for s in sets:
                 tq.sdpa_int4(q, *s, Hq // Hkv, 1.0, W, out=out)
         # warm the capture stream up eagerly, so its split-K workspace exists
-        # before capture (nothing is allocated inside the graph)
+        # before capture (nothing is allocated inside the graphs)
         cs = torch.cuda.Stream()
         with torch.cuda.stream(cs):
-            one_step()
+            one_step(steps_kv[0])
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=cs):
-            one_step()
-        ms_step, ms_launch, _ = time_launches(torch, lambda i: g.replay(), args.steps, args.warmup)
+        graphs = []
+        for sets in steps_kv:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cs):
+                one_step(sets)
+            graphs.append(g)
+        ms_step, ms_launch, _ = time_launches(torch, lambda i: graphs[i % nsteps].replay(),
+                                              args.steps, args.warmup)
         us_layer = ms_step * 1e3 / layers
         gbs = nbytes * layers / (ms_step * 1e-3) / 1e9
         emit({"metric": "int4-KV decode SDPA, 50 sliding layers (HIP graph) GB/s",
@@ -332,7 +357,9 @@ def main():
               "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
               "us_per_layer": round(us_layer, 3), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-              "dtype": precision_note(args.sb), "data": "synthetic",
+              "dtype": precision_note(args.sb),
+              "data": f"synthetic; {nsteps} distinct 50-layer KV sets rotated "
+                      f"({nsteps * layers * layer_bytes / 2**20:.0f} MiB, more than the 256 MB MALL)",
               "config": {"workload": "50 x sdpa_int4 Hq=32 Hkv=16 D=256 L=786 W=1024, "
                                      f"{args.sb} scale/bias (BASELINE configs[1]), one HIP graph "
                                      "per step",

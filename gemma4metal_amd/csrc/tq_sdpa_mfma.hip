@@ -341,17 +341,29 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
   for (int s = 0; s < NCH; ++s) {
     const int ch = lane + 64 * s;
     const bool ok = ch < G * D / 8;
+    // (one uniform dtype branch per chunk, straight-line conversions inside)
     float f[8];
-    const uint32_t w16[4] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w};
-    const uint32_t w32[8] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w, qb[s].x, qb[s].y, qb[s].z, qb[s].w};
+    if (q32) {
+      const uint32_t w[8] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w, qb[s].x, qb[s].y, qb[s].z, qb[s].w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t h16 = (w16[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      const float x = q32 ? __uint_as_float(w32[e])
-                      : p.q_dtype == TQ_F16 ? __half2float(__ushort_as_half(static_cast<uint16_t>(h16)))
-                                            : __uint_as_float(h16 << 16);
-      f[e] = ok ? x * p.scale_log2 : 0.0f;
+      for (int e = 0; e < 8; ++e) f[e] = __uint_as_float(w[e]);
+    } else if (p.q_dtype == TQ_F16) {
+      const uint32_t w[4] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = half_lo(w[e]);
+        f[2 * e + 1] = half_hi(w[e]);
+      }
+    } else {
+      const uint32_t w[4] = {qa[s].x, qa[s].y, qa[s].z, qa[s].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[2 * e] = __uint_as_float(w[e] << 16);
+        f[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+      }
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = ok ? f[e] * p.scale_log2 : 0.0f;
     float amax = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
@@ -361,31 +373,36 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     if (amax > 0.0f) frexpf(amax, &ex);  // amax < 2^ex
     const int F = 22 - ex;               // |round(q * 2^F)| <= 2^22
     const float sF = ldexpf(1.0f, F);
-    int X[8], xs = 0;
+    // three signed base-256 digits per element: the low byte of X, then of
+    // X1 = (X - sext(byte)) / 256, then of X2 = (X1 - sext(byte)) / 256
+    uint32_t dg[3][8];
+    int xs = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      X[e] = static_cast<int>(__builtin_rintf(f[e] * sF));
-      xs += X[e];
+      const int X = static_cast<int>(__builtin_rintf(f[e] * sF));
+      xs += X;
+      const int X1 = (X - __builtin_amdgcn_sbfe(X, 0, 8)) >> 8;
+      const int X2 = (X1 - __builtin_amdgcn_sbfe(X1, 0, 8)) >> 8;
+      dg[0][e] = static_cast<uint32_t>(X);
+      dg[1][e] = static_cast<uint32_t>(X1);
+      dg[2][e] = static_cast<uint32_t>(X2);
     }
     // sum over the quant group's 64 dims (8 lanes), exact: 64 * 2^22 < 2^31
     xs = group_sum_i<8>(xs);
     Fs[s] = F;
     qhs[s] = static_cast<float>(xs) * ldexpf(1.0f, -F);
-    // three signed base-256 digits per element; bytes of elements 0, 2, 4, 6
-    // (even) and 1, 3, 5, 7 (odd) form two dwords of the 16 k-slots of
-    // this chunk's MFMA, lane group and column
-    uint32_t ev[3] = {0u, 0u, 0u}, od[3] = {0u, 0u, 0u};
+    // the low bytes of elements 0, 2, 4, 6 (even) and 1, 3, 5, 7 (odd) form
+    // two dwords of the 16 k-slots of this chunk's MFMA, lane group and
+    // column (three byte permutes per dword)
+    uint32_t ev[3], od[3];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d0 = static_cast<int8_t>(X[e] & 0xFF);
-      const int X1 = (X[e] - d0) >> 8;
-      const int d1 = static_cast<int8_t>(X1 & 0xFF);
-      const int d2 = (X1 - d1) >> 8;
-      const int sh = 8 * (e >> 1);
-      uint32_t* dst = (e & 1) ? od : ev;
-      dst[0] |= static_cast<uint32_t>(d0 & 0xFF) << sh;
-      dst[1] |= static_cast<uint32_t>(d1 & 0xFF) << sh;
-      dst[2] |= static_cast<uint32_t>(d2 & 0xFF) << sh;
+    for (int k = 0; k < 3; ++k) {
+      const uint32_t e02 = __builtin_amdgcn_perm(dg[k][2], dg[k][0], 0x0C0C0400u);
+      const uint32_t e46 = __builtin_amdgcn_perm(dg[k][6], dg[k][4], 0x0C0C0400u);
+      const uint32_t o13 = __builtin_amdgcn_perm(dg[k][3], dg[k][1], 0x0C0C0400u);
+      const uint32_t o57 = __builtin_amdgcn_perm(dg[k][7], dg[k][5], 0x0C0C0400u);
+      ev[k] = __builtin_amdgcn_perm(e46, e02, 0x05040100u);
+      od[k] = __builtin_amdgcn_perm(o57, o13, 0x05040100u);
     }
     if (ok) {
       const int v = 8 * ch / D, dim0 = 8 * ch - v * D;
