@@ -427,7 +427,7 @@ __global__ __launch_bounds__(256) void polar16_sdpa_kernel(SdpaParams p, Attn16 
   __shared__ float2 cst[1024];
   __shared__ __align__(16) float qs[G * D];
   using Fin = Finalize<G, D, NW>;
-  __shared__ float arena[Fin::kArena];
+  __shared__ __align__(16) float arena[Fin::kArena];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hy = blockIdx.y, split = blockIdx.x;
   const int kvh = hy / p.n_sub, sub = hy - kvh * p.n_sub;
@@ -1285,7 +1285,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   constexpr int D = 128;
   __shared__ P7Tables<G> T;
   using Fin = Finalize<G, D, NW>;
-  __shared__ float arena[Fin::kArena];
+  __shared__ __align__(16) float arena[Fin::kArena];
   __shared__ float p_lds[NW][G][64];   // [wave][head][slot]
   __shared__ float sv_lds[NW][2][64];  // [wave][quant group][slot] V scale
   __shared__ float bv_lds[NW][2][64];  // V bias
@@ -1724,6 +1724,8 @@ int polar_sdpa_params(SdpaParams& p, int Hq, int Hkv, int D, int n, int cap, flo
   const int chunk = polar_chunk(eff, groups);
   const int max_splits = polar_splits_bound(eff, groups);
   const WsLayout wl = ws_layout(1, Hq, D, max_splits);
+  // the split partials are addressed with 32-bit byte offsets
+  TQ_CHECK_ARG(wl.total - wl.o_off < (size_t{1} << 31), "%s: split-K partials exceed 2 GiB", fn);
   if (max_splits > 1 && (!workspace || ws_bytes < wl.total)) {
     set_error("%s: workspace of %zu bytes needed (got %zu)", fn, wl.total, ws_bytes);
     return TQ_ERR_WORKSPACE;

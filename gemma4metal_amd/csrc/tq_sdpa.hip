@@ -460,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void sdpa_int4_kernel(SdpaParams p) {
   }
 
   using Fin = Finalize<G, D>;
-  __shared__ float arena[Fin::kArena];
+  __shared__ __align__(16) float arena[Fin::kArena];
   if (tok == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -531,6 +531,8 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
       return TQ_ERR_WORKSPACE;
     }
     TQ_CHECK_ARG(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "%s: workspace must be 16-byte aligned", fn);
+    // the split partials are addressed with 32-bit byte offsets
+    TQ_CHECK_ARG(wl.total - wl.o_off < (size_t{1} << 31), "%s: split-K partials exceed 2 GiB", fn);
   }
   TQ_CHECK_ARG(Hkv * n_sub <= 65535 && batch <= 65535, "%s: grid too large", fn);
   TQ_CHECK_ARG(static_cast<int64_t>(batch) * Hq <= kMaxCounters || (prefill && max_splits == 1),

@@ -257,6 +257,38 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// VEC (2 or 4) consecutive floats as one agent-scope (sc1) 8- or 16-byte
+// buffer access, the cache policy of the relaxed agent-scope atomics above.
+constexpr int kBufSc1 = 16;  // buffer instruction cache-policy bits: sc1
+template <int VEC>
+struct CoherentVec {
+  static_assert(VEC == 1 || VEC == 2 || VEC == 4, "VEC");
+  typedef float FV __attribute__((ext_vector_type(VEC)));
+  typedef uint32_t UV __attribute__((ext_vector_type(VEC)));
+  __device__ static __amdgpu_buffer_rsrc_t rsrc(float* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7FFFFFFF, 0x00020000);
+  }
+  __device__ static FV load(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    FV v;
+    if constexpr (VEC == 1) {
+      v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kBufSc1));
+    } else if constexpr (VEC == 2) {
+      v = __builtin_bit_cast(FV, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kBufSc1));
+    } else {
+      v = __builtin_bit_cast(FV, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kBufSc1));
+    }
+    return v;
+  }
+  __device__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, FV v) {
+    if constexpr (VEC == 1)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, byte_off, 0, kBufSc1);
+    else if constexpr (VEC == 2)
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(UV, v), r, byte_off, 0, kBufSc1);
+    else
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(UV, v), r, byte_off, 0, kBufSc1);
+  }
+};
+
 // A split's (m, l) pair as one 8-byte access (p 8-byte aligned).
 __device__ __forceinline__ void store_coherent_pair(float* p, float m, float l) {
   const uint64_t v = static_cast<uint64_t>(__float_as_uint(m)) | (static_cast<uint64_t>(__float_as_uint(l)) << 32);
@@ -363,15 +395,30 @@ struct Finalize {
                              int nvalid = G) {
     static_assert(D % 64 == 0, "one head per wave");
     static_assert(NW <= 16, "per-wave partials fit one row of 16 lanes");
-    constexpr int NI = (G * D + kNT - 1) / kNT;  // outputs per thread
+    // A thread takes VEC consecutive dims of one head: the arena rows are
+    // read as VEC-float LDS vectors and the split partials move as one 4-,
+    // 8- or 16-byte agent-scope access per split (fewer memory instructions,
+    // which the CU's address unit serialises).  VEC is as large as keeps
+    // every wave busy (G * D / threads outputs each; concentrating the
+    // combine on fewer waves was slower) and at most 4, and a wave's
+    // 64 * VEC dims lie in one head.
+    constexpr int VPT = G * D / kNT;  // outputs per thread
+    constexpr int VEC = (VPT >= 4 && D >= 256) ? 4 : ((VPT >= 2 && D >= 128) ? 2 : 1);
+    using CV = CoherentVec<VEC>;
+    using FV = float __attribute__((ext_vector_type(VEC)));
+    constexpr int NU = G * D / VEC;             // (head, dim vector) units
+    constexpr int NI = (NU + kNT - 1) / kNT;    // units per thread
     auto row = [&](int h) -> int64_t { return head_base + (h / gh) * qstride + h % gh; };
     const int lane = threadIdx.x & 63;
+    // split partials: [row][split][D] floats, byte offsets below 2^31
+    // (checked on the host)
+    const __amdgpu_buffer_rsrc_t wso = CV::rsrc(p.ws_o);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int idx = threadIdx.x + i * kNT;
-      const int h = idx / D, d = idx - (idx / D) * D;
-      if (idx >= G * D || h >= nvalid) continue;  // wave-uniform
+      const int u = threadIdx.x + i * kNT;
+      const int h = u * VEC / D, d = u * VEC - (u * VEC / D) * D;
+      if (u >= NU || h >= nvalid) continue;  // wave-uniform
       // lane w < NW: wave w's (m, l) of head h (each row of 16 lanes holds
       // the same copy, so a row reduction is the workgroup's)
       const int w = lane & 15;
@@ -380,27 +427,37 @@ struct Finalize {
       const float M = row16_max(mw);
       const float fw = merge_factor(mw, M);
       const float Ls = group_sum<16>(lw * fw);
-      float O = 0.0f;
-      if constexpr (CORR) {
-        // the corrections of this wave's group (d / 64 is wave-uniform)
-        float cw = 0.0f;
-        if (w < NW) {
+      FV O;
+      {
+        float c0 = 0.0f;
+        if constexpr (CORR) {
+          // the corrections of this wave's group (d / 64 is wave-uniform)
+          float cw = 0.0f;
+          if (w < NW) {
 #pragma unroll
-          for (int t = 0; t < SPW; ++t) cw += corr(arena, w * SPW + t)[h * NGc + d / 64];
+            for (int t = 0; t < SPW; ++t) cw += corr(arena, w * SPW + t)[h * NGc + d / 64];
+          }
+          c0 = group_sum<16>(cw * fw);
         }
-        O = group_sum<16>(cw * fw);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) O[e] = c0;
       }
 #pragma unroll
       for (int k = 0; k < NW; ++k) {
         const float fk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fw), k));
 #pragma unroll
-        for (int t = 0; t < SPW; ++t) O = fmaf(o(arena, k * SPW + t, h)[d], fk, O);
+        for (int t = 0; t < SPW; ++t) {
+          const FV ov = *reinterpret_cast<const FV*>(o(arena, k * SPW + t, h) + d);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) O[e] = fmaf(ov[e], fk, O[e]);
+        }
       }
       if (S == 1) {
-        p.out[row(h) * D + d] = normalise(O, Ls, p.denom_eps);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) p.out[row(h) * D + d + e] = normalise(O[e], Ls, p.denom_eps);
       } else {
         const int64_t slot = row(h) * p.max_splits + split;
-        store_coherent(p.ws_o + slot * D + d, O);
+        CV::store(wso, static_cast<uint32_t>((slot * D + d) * 4), O);
         if (d == 0) store_coherent_pair(p.ws_ml + slot * 2, M, Ls);
       }
     }
@@ -434,28 +491,33 @@ struct Finalize {
     if (!s_last) return;
 
     // Merge, KC splits at a time: lane k (mod 16) loads split s0 + k's
-    // (m, l), and every lane the KC partials of its outputs (coalesced over
-    // dims).  All loads of a chunk, for all of a thread's outputs, go out
-    // before the first use: one memory round trip per chunk, one in all for
-    // S <= KC.
+    // (m, l), and every thread the KC partial vectors of its units.  All
+    // loads of a chunk, for all of a thread's units, go out before the first
+    // use: one memory round trip per chunk, one in all for S <= KC.
     constexpr int KC = 16;
-    float Mr[NI], Lr[NI], Or[NI];
+    float Mr[NI], Lr[NI];
+    FV Or[NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) { Mr[i] = -INFINITY; Lr[i] = 0.0f; Or[i] = 0.0f; }
+    for (int i = 0; i < NI; ++i) {
+      Mr[i] = -INFINITY;
+      Lr[i] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) Or[i][e] = 0.0f;
+    }
     for (int s0 = 0; s0 < S; s0 += KC) {
       float2 mlv[NI];
-      float ok[NI][KC];
+      FV ok[NI][KC];
       const int sl = min(s0 + (lane & (KC - 1)), S - 1);
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
-        const int idx = threadIdx.x + i * kNT;
-        // (past the last output: a valid row, loaded and dropped below)
-        const int h = min(idx / D, nvalid - 1), d = idx - (idx / D) * D;
+        const int u = min(static_cast<int>(threadIdx.x) + i * kNT, NU - 1);
+        // (past the last unit: a valid row, loaded and dropped below)
+        const int h = min(u * VEC / D, nvalid - 1), d = u * VEC - (u * VEC / D) * D;
         mlv[i] = load_coherent_pair(p.ws_ml + (row(h) * p.max_splits + sl) * 2);
-        const float* po = p.ws_o + row(h) * p.max_splits * D + d;
+        const int64_t base = row(h) * p.max_splits * D + d;
 #pragma unroll
         for (int k = 0; k < KC; ++k)
-          ok[i][k] = load_coherent(po + static_cast<int64_t>(min(s0 + k, S - 1)) * D);
+          ok[i][k] = CV::load(wso, static_cast<uint32_t>((base + static_cast<int64_t>(min(s0 + k, S - 1)) * D) * 4));
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -465,20 +527,24 @@ struct Finalize {
         const float fr = merge_factor(Mr[i], Mn);
         const float fk = merge_factor(mk, Mn);
         Lr[i] = fmaf(Lr[i], fr, group_sum<16>(mlv[i].y * fk));
-        float O = Or[i] * fr;
+        FV O = Or[i] * fr;
 #pragma unroll
-        for (int k = 0; k < KC; ++k)
-          O = fmaf(ok[i][k], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fk), k)), O);
+        for (int k = 0; k < KC; ++k) {
+          const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fk), k));
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) O[e] = fmaf(ok[i][k][e], f, O[e]);
+        }
         Or[i] = O;
         Mr[i] = Mn;
       }
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int idx = threadIdx.x + i * kNT;
-      const int h = idx / D, d = idx - (idx / D) * D;
-      if (idx >= G * D || h >= nvalid) continue;
-      p.out[row(h) * D + d] = normalise(Or[i], Lr[i], p.denom_eps);
+      const int u = threadIdx.x + i * kNT;
+      const int h = u * VEC / D, d = u * VEC - (u * VEC / D) * D;
+      if (u >= NU || h >= nvalid) continue;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) p.out[row(h) * D + d + e] = normalise(Or[i][e], Lr[i], p.denom_eps);
     }
   }
 };
