@@ -515,9 +515,22 @@ struct Finalize {
         const int h = min(u * VEC / D, nvalid - 1), d = u * VEC - (u * VEC / D) * D;
         mlv[i] = load_coherent_pair(p.ws_ml + (row(h) * p.max_splits + sl) * 2);
         const int64_t base = row(h) * p.max_splits * D + d;
+        // only the chunk's existing splits are loaded (a clamped duplicate
+        // load would still take an address-unit slot); full chunks without
+        // the per-split branches
+        if (s0 + KC <= S) {
 #pragma unroll
-        for (int k = 0; k < KC; ++k)
-          ok[i][k] = CV::load(wso, static_cast<uint32_t>((base + static_cast<int64_t>(min(s0 + k, S - 1)) * D) * 4));
+          for (int k = 0; k < KC; ++k)
+            ok[i][k] = CV::load(wso, static_cast<uint32_t>((base + static_cast<int64_t>(s0 + k) * D) * 4));
+        } else {
+#pragma unroll
+          for (int k = 0; k < KC; ++k) {
+            if (s0 + k < S)
+              ok[i][k] = CV::load(wso, static_cast<uint32_t>((base + static_cast<int64_t>(s0 + k) * D) * 4));
+            else
+              ok[i][k] = FV{};
+          }
+        }
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
