@@ -349,7 +349,10 @@ def main():
               "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
               "us_per_layer": round(ms_step * 1e3, 2), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-              "dtype": precision_note(args.sb), "data": "synthetic",
+              "dtype": precision_note(args.sb),
+              "data": (f"synthetic; {nsets} rotated KV sets "
+                       f"({nsets * Hkvg * L * O.row_bytes(Dg, sb_bytes) / 2**20:.0f} MiB, more than "
+                       "the 256 MB MALL)"),
               "kernel": plan["kernel"], "splits": plan["splits"],
               "config": {"workload": f"sdpa_int4 Hq={Hg} Hkv={Hkvg} D={Dg} L={L} W=0, {args.sb} "
                                      "scale/bias (global layer)",
@@ -553,7 +556,7 @@ def bench_polar(args, torch, gen):
     P = P.to(torch.float32).contiguous()
     S = torch.randn((128, D), generator=gen, device="cuda")
     codec = pq.Polar7Codec(P, S)
-    nsets = args.sets
+    nsets = rotation_sets(args.sets, Hkv * L * 140)  # 140 B per (kv head, key)
     sets = []
     for _ in range(nsets):
         k = torch.randn((Hkv, L, D), generator=gen, device="cuda")
@@ -604,7 +607,8 @@ def bench_polar(args, torch, gen):
           "dtype": "polar7 angles + 128-bit QJL sketch (fp16 norms), int4 V (fp16 scale/bias), "
                    "f32 q, f32 accumulate",
           "data": f"synthetic (seeded N(0,1) K/V/q, seeded orthogonal P and N(0,1) S); "
-                  f"{nsets} rotated KV sets",
+                  f"{nsets} rotated KV sets ({nsets * Hkv * L * 140 / 2**20:.0f} MiB, more than the "
+                  f"256 MB MALL)",
           "config": {"workload": f"polar7+QJL decode layer Hq={Hq} Hkv={Hkv} D={D} L={L} "
                                  "(BASELINE configs[4])", "global_batch": 1, "seq_len": L,
                      "parallelism": "none (1 GPU)"},
