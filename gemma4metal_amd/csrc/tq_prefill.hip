@@ -71,37 +71,80 @@ __device__ __forceinline__ float sbf(float x) { return x; }
 // Dequantization of one tile's raw words (this thread's keys) into the LDS
 // images: K as fp16 hi / lo rows, V^T as bf16 hi / lo (value s * n + b in
 // fp32, then its rounded high part and the rounded remainder).
+// Nibbles of a word as floats: the low and high nibble of each byte are
+// masked into bytes of their own and converted by byte (v_cvt_f32_ubyte0-3),
+// so no nibble needs a shift of its own.  Element i of the word is bits 4i.
+__device__ __forceinline__ void pf_nibbles(uint32_t wd, float (&n)[8]) {
+  uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+  // opaque: otherwise each byte conversion is folded back into a shift and
+  // a mask of the raw word
+  asm("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    n[2 * b] = static_cast<float>((lo >> (8 * b)) & 0xFFu);
+    n[2 * b + 1] = static_cast<float>((hi >> (8 * b)) & 0xFFu);
+  }
+}
+
+// The fp16 remainders x0 - h0, x1 - h1 of a pair whose fp16 high parts are
+// packed in hp, as a packed fp16 pair: one mixed-precision fma each (fp16
+// source, fp32 addend, fp16 result into the low / high half).  The
+// remainder is exact in fp32 and rounded once, to fp16.
+__device__ __forceinline__ uint32_t pf_rem_pair(uint32_t hp, float x0, float x1) {
+  uint32_t r;
+  asm volatile(
+      "v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(r)
+      : "v"(hp), "v"(x0), "v"(x1));
+  return r;
+}
+
 template <int D, bool F32>
 __device__ __forceinline__ void pf_dequant(const PfRaw<D, F32>& raw, _Float16* khi, _Float16* klo, __bf16* vthi,
                                            __bf16* vtlo, int w, int kb0, int wv, int kv0) {
   using Gm = PfGeom<D>;
   constexpr int KSTR = Gm::KSTR, VSTR = Gm::VSTR, KPT = Gm::KPT;
+  typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int e = 0; e < KPT; ++e) {
     const int key = kb0 + e;
     const float ks = sbf(raw.ks[e]), kbias = sbf(raw.kb[e]);
-    v8h kh, kl;
+    float n[8];
+    pf_nibbles(raw.kw[e], n);
+    u32x4 kh, kl;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float x = fmaf(ks, static_cast<float>((raw.kw[e] >> (4 * j)) & 15u), kbias);
-      const _Float16 h = static_cast<_Float16>(x);
-      kh[j] = h;
-      kl[j] = static_cast<_Float16>(x - static_cast<float>(h));
+    for (int q = 0; q < 4; ++q) {
+      const float x0 = fmaf(ks, n[2 * q], kbias), x1 = fmaf(ks, n[2 * q + 1], kbias);
+      const uint32_t hp = __builtin_bit_cast(uint32_t, v2h{static_cast<_Float16>(x0), static_cast<_Float16>(x1)});
+      kh[q] = hp;
+      kl[q] = pf_rem_pair(hp, x0, x1);
     }
-    *reinterpret_cast<v8h*>(&khi[key * KSTR + 8 * w]) = kh;
-    *reinterpret_cast<v8h*>(&klo[key * KSTR + 8 * w]) = kl;
+    *reinterpret_cast<u32x4*>(&khi[key * KSTR + 8 * w]) = kh;
+    *reinterpret_cast<u32x4*>(&klo[key * KSTR + 8 * w]) = kl;
   }
-  // V^T: the KPT keys of one dim are adjacent -- one 4 / 8 / 16 B store each
+  // V^T: the KPT keys of one dim are adjacent -- one 4 / 8 / 16 B store each;
+  // the bf16 high and low parts of a key pair each take one packed conversion
   typedef __bf16 vkpt __attribute__((ext_vector_type(KPT)));
+  typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+  float nv[KPT][8];
+#pragma unroll
+  for (int e = 0; e < KPT; ++e) pf_nibbles(raw.vw[e], nv[e]);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     vkpt vh, vl;
 #pragma unroll
-    for (int e = 0; e < KPT; ++e) {
-      const float x = fmaf(sbf(raw.vs[e]), static_cast<float>((raw.vw[e] >> (4 * j)) & 15u), sbf(raw.vb[e]));
-      const __bf16 h = static_cast<__bf16>(x);
-      vh[e] = h;
-      vl[e] = static_cast<__bf16>(x - static_cast<float>(h));
+    for (int e = 0; e < KPT; e += 2) {
+      const float x0 = fmaf(sbf(raw.vs[e]), nv[e][j], sbf(raw.vb[e]));
+      const float x1 = fmaf(sbf(raw.vs[e + 1]), nv[e + 1][j], sbf(raw.vb[e + 1]));
+      const v2bf_t h = v2bf_t{static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
+      const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+      const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xFFFF0000u);
+      const v2bf_t l = v2bf_t{static_cast<__bf16>(x0 - h0), static_cast<__bf16>(x1 - h1)};
+      vh[e] = h[0];
+      vh[e + 1] = h[1];
+      vl[e] = l[0];
+      vl[e + 1] = l[1];
     }
     *reinterpret_cast<vkpt*>(&vthi[(8 * wv + j) * VSTR + kv0]) = vh;
     *reinterpret_cast<vkpt*>(&vtlo[(8 * wv + j) * VSTR + kv0]) = vl;
