@@ -6,9 +6,10 @@
 // A workgroup takes all gqa heads of one kv head for 64 / gqa consecutive
 // queries (16 rows per wave) and streams the union of their key ranges in
 // tiles of 32 keys.  Each tile is dequantized once into LDS:
-//   K as fp16 hi / lo rows [key][dim], V transposed as bf16 hi / lo [dim][key]
+//   K as fp16 hi / lo rows [key][dim], V transposed as bf16 hi / lo [dim][slot]
 // (value = s * nibble + b in fp32, split into a rounded high part and the
-// rounded remainder).
+// rounded remainder).  V^T slot 8c + 4h + j holds key 16h + 4c + j, so the
+// eight keys lane group c weights (below) are one 16 B read.
 // Per tile and wave, on the matrix cores (l = lane, m = l % 16, c = l / 16):
 //   S^T = K q^T   v_mfma_f32_16x16x32_f16, A = 16 keys x 32 dims of K, B =
 //                 32 dims x 16 rows of q (hi / lo in registers); the three
@@ -44,8 +45,9 @@ struct PfGeom {
   static constexpr int W = D / 8;                     // packed words per row
   static constexpr int KSTR = D + 8;                  // K rows in LDS (halves; 16 B pad)
   static constexpr int KPT = kPfKeys * W / kPfThreads;  // keys per thread in the dequant
-  // V^T rows in LDS (halves): KPT-key stores stay aligned, rows padded
-  static constexpr int VSTR = KPT == 8 ? kPfKeys + 8 : kPfKeys + 4;
+  // V^T rows in LDS (halves): 16 B aligned for the 8-slot reads; a 16-row
+  // read phase at this stride (20 dwords) covers all 64 banks once
+  static constexpr int VSTR = kPfKeys + 8;
   static constexpr int CH = D / 32;                   // K.q k-steps of 32 dims
   static constexpr int DB = D / 16;                   // 16-dim output blocks
   static_assert(KPT == 2 || KPT == 4 || KPT == 8, "D");
@@ -60,14 +62,18 @@ struct PfRaw {
   SB ks[PfGeom<D>::KPT], kb[PfGeom<D>::KPT], vs[PfGeom<D>::KPT], vb[PfGeom<D>::KPT];
 };
 
+// The key (0 .. 31 within the tile) held by V^T slot s.
+__device__ __forceinline__ int pf_vkey(int s) { return 16 * ((s >> 2) & 1) + 4 * (s >> 3) + (s & 3); }
+
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 __device__ __forceinline__ float sbf(uint16_t h) { return h2f(h); }
 __device__ __forceinline__ float sbf(float x) { return x; }
 
-// K and V use different thread roles (word w, keys k0 .. k0 + KPT - 1): K's
-// lanes run along the words of a key (its LDS rows are key-major), V's
-// along the keys of a word (V^T rows are dim-major), so that both LDS
-// stores of a 16-lane phase land in distinct banks.
+// K and V use different thread roles (word w, keys k0 .. k0 + KPT - 1 for
+// K, V^T slots k0 .. k0 + KPT - 1 for V): K's lanes run along the words of a
+// key (its LDS rows are key-major), V's along the slots of a word (V^T rows
+// are dim-major), so that both LDS stores of a 16-lane phase land in
+// distinct banks.
 // Dequantization of one tile's raw words (this thread's keys) into the LDS
 // images: K as fp16 hi / lo rows, V^T as bf16 hi / lo (value s * n + b in
 // fp32, then its rounded high part and the rounded remainder).
@@ -123,7 +129,7 @@ __device__ __forceinline__ void pf_dequant(const PfRaw<D, F32>& raw, _Float16* k
     *reinterpret_cast<u32x4*>(&khi[key * KSTR + 8 * w]) = kh;
     *reinterpret_cast<u32x4*>(&klo[key * KSTR + 8 * w]) = kl;
   }
-  // V^T: the KPT keys of one dim are adjacent -- one 4 / 8 / 16 B store each;
+  // V^T: the KPT slots of one dim are adjacent -- one 4 / 8 / 16 B store each;
   // the bf16 high and low parts of a key pair each take one packed conversion
   typedef __bf16 vkpt __attribute__((ext_vector_type(KPT)));
   typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
@@ -159,7 +165,8 @@ __device__ __forceinline__ void pf_load(PfRaw<D, F32>& R, const SdpaParams& p, i
 #pragma unroll
   for (int e = 0; e < Gm::KPT; ++e) {
     const int64_t rk = row0 + min(t0 + kk0 + e, last);
-    const int64_t rv = row0 + min(t0 + kv0 + e, last);
+    // slots kv0 .. kv0 + KPT - 1 hold keys vkey(kv0) + e % 4 + 16 (e / 4)
+    const int64_t rv = row0 + min(t0 + pf_vkey(kv0) + (e & 3) + 16 * (e >> 2), last);
     R.kw[e] = __builtin_nontemporal_load(p.kq + rk * Gm::W + wk);
     R.vw[e] = __builtin_nontemporal_load(p.vq + rv * Gm::W + wv);
     R.ks[e] = static_cast<const SB*>(p.ks)[rk * (D / 64) + (wk >> 3)];
@@ -233,7 +240,7 @@ void prefill_int4_kernel(SdpaParams p) {
   }
 
   // dequant roles: word w of keys kb0 .. kb0 + KPT - 1 of a tile (K), word
-  // wv of keys kv0 .. (V)
+  // wv of V^T slots kv0 .. (V)
   constexpr int KB = kPfKeys / KPT;  // key blocks per tile
   const int w = threadIdx.x % W, kb0 = (threadIdx.x / W) * KPT;
   const int wv = threadIdx.x / KB, kv0 = (threadIdx.x % KB) * KPT;
@@ -308,18 +315,25 @@ void prefill_int4_kernel(SdpaParams p) {
     const v8bf bl = v8bf{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
 
     // ---- O^T += V^T P^T ------------------------------------------------------
+    // four blocks' V^T reads issued ahead of their products (the compiler
+    // otherwise keeps one block's reads in flight)
 #pragma unroll
-    for (int b = 0; b < DB; ++b) {
-      const int off = (16 * b + m) * VSTR + 4 * c;
-      const u32x2 h0 = *reinterpret_cast<const u32x2*>(&vthi[off]);
-      const u32x2 h1 = *reinterpret_cast<const u32x2*>(&vthi[off + 16]);
-      const u32x2 l0 = *reinterpret_cast<const u32x2*>(&vtlo[off]);
-      const u32x2 l1 = *reinterpret_cast<const u32x2*>(&vtlo[off + 16]);
-      const v8bf ah = __builtin_bit_cast(v8bf, u32x4{h0.x, h0.y, h1.x, h1.y});
-      const v8bf al = __builtin_bit_cast(v8bf, u32x4{l0.x, l0.y, l1.x, l1.y});
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[b], 0, 0, 0);
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[b], 0, 0, 0);
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[b], 0, 0, 0);
+    for (int b0 = 0; b0 < DB; b0 += 4) {
+      v8bf ah[4], al[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int off = (16 * (b0 + j) + m) * VSTR + 8 * c;
+        ah[j] = *reinterpret_cast<const v8bf*>(&vthi[off]);
+        al[j] = *reinterpret_cast<const v8bf*>(&vtlo[off]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = b0 + j;
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[j], bh, o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[j], bl, o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[j], bh, o[b], 0, 0, 0);
+      }
     }
   };
   if constexpr (NB == 2) {
@@ -494,18 +508,25 @@ void prefill_int4_ws_kernel(SdpaParams p) {
     const v8bf bh = v8bf{ph[0], ph[1], ph[2], ph[3], ph[4], ph[5], ph[6], ph[7]};
     const v8bf bl = v8bf{pl[0], pl[1], pl[2], pl[3], pl[4], pl[5], pl[6], pl[7]};
     // ---- O^T += V^T P^T ------------------------------------------------------
+    // four blocks' V^T reads issued ahead of their products (the compiler
+    // otherwise keeps one block's reads in flight)
 #pragma unroll
-    for (int b = 0; b < DB; ++b) {
-      const int off = (16 * b + m) * VSTR + 4 * c;
-      const u32x2 h0 = *reinterpret_cast<const u32x2*>(&vh_[off]);
-      const u32x2 h1 = *reinterpret_cast<const u32x2*>(&vh_[off + 16]);
-      const u32x2 l0 = *reinterpret_cast<const u32x2*>(&vl_[off]);
-      const u32x2 l1 = *reinterpret_cast<const u32x2*>(&vl_[off + 16]);
-      const v8bf ah = __builtin_bit_cast(v8bf, u32x4{h0.x, h0.y, h1.x, h1.y});
-      const v8bf al = __builtin_bit_cast(v8bf, u32x4{l0.x, l0.y, l1.x, l1.y});
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[b], 0, 0, 0);
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[b], 0, 0, 0);
-      o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[b], 0, 0, 0);
+    for (int b0 = 0; b0 < DB; b0 += 4) {
+      v8bf ah[4], al[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int off = (16 * (b0 + j) + m) * VSTR + 8 * c;
+        ah[j] = *reinterpret_cast<const v8bf*>(&vh_[off]);
+        al[j] = *reinterpret_cast<const v8bf*>(&vl_[off]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = b0 + j;
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[j], bh, o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[j], bl, o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[j], bh, o[b], 0, 0, 0);
+      }
     }
   };
 
