@@ -188,6 +188,7 @@ void prefill_int4_kernel(SdpaParams p) {
   constexpr int KPT = Gm::KPT;
   __shared__ __attribute__((aligned(16))) _Float16 khi[kPfKeys * KSTR], klo[kPfKeys * KSTR];
   __shared__ __attribute__((aligned(16))) __bf16 vthi[D * VSTR], vtlo[D * VSTR];
+  static_assert(DB % 4 == 0, "V^T reads are issued four blocks ahead");
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;
@@ -375,6 +376,7 @@ void prefill_int4_ws_kernel(SdpaParams p) {
   constexpr int W = Gm::W, KSTR = Gm::KSTR, VSTR = Gm::VSTR, CH = Gm::CH, DB = Gm::DB;
   constexpr int KPT = Gm::KPT;
   constexpr int KI = kPfKeys * KSTR, VI = D * VSTR;  // halves per K / V^T image
+  static_assert(CH % 4 == 0 && DB % 4 == 0, "reads are issued four k-steps / blocks ahead");
   __shared__ __attribute__((aligned(16))) _Float16 khi[2][KI], klo[2][KI];
   __shared__ __attribute__((aligned(16))) __bf16 vthi[2][VI], vtlo[2][VI];
 
@@ -416,6 +418,9 @@ void prefill_int4_ws_kernel(SdpaParams p) {
   }
 
   // =================== compute waves: S^T, softmax, O^T ======================
+  // the compute waves bind each step: they win issue over the loader waves
+  // sharing their SIMDs
+  __builtin_amdgcn_s_setprio(3);
   // this lane's row (column m of its wave): query q0 + r / gqa, head r % gqa
   const int r = 16 * (wave - kPfWaves) + m;
   const int qo = r / gqa, ho = r - qo * gqa;
@@ -465,14 +470,23 @@ void prefill_int4_ws_kernel(SdpaParams p) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      // K reads of four k-steps issued ahead of their products
 #pragma unroll
-      for (int ch = 0; ch < CH; ++ch) {
-        const int off = (16 * half + m) * KSTR + 32 * ch + 8 * c;
-        const v8h ah = *reinterpret_cast<const v8h*>(&kh_[off]);
-        const v8h al = *reinterpret_cast<const v8h*>(&kl_[off]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[ch], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ch], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[ch], acc, 0, 0, 0);
+      for (int c0 = 0; c0 < CH; c0 += 4) {
+        v8h ah[4], al[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int off = (16 * half + m) * KSTR + 32 * (c0 + j) + 8 * c;
+          ah[j] = *reinterpret_cast<const v8h*>(&kh_[off]);
+          al[j] = *reinterpret_cast<const v8h*>(&kl_[off]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], qh[c0 + j], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], ql[c0 + j], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], qh[c0 + j], acc, 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
