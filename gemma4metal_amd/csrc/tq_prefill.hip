@@ -51,16 +51,28 @@ struct PfGeom {
   static constexpr int CH = D / 32;                   // K.q k-steps of 32 dims
   static constexpr int DB = D / 16;                   // 16-dim output blocks
   static_assert(KPT == 2 || KPT == 4 || KPT == 8, "D");
+  // D = 512: each lane loads one scale and one bias value of a tile per
+  // tensor, and the dequantization takes the ones its keys need from the
+  // lanes that hold them (ds_bpermute): 4 loads and registers instead of 32
+  // while the tile's words are in flight
+  static constexpr bool LANE_SB = D == 512;
+  static constexpr int NS = LANE_SB ? 1 : KPT;
+  static_assert(!LANE_SB || (W == 64 && KPT == 8 && kPfThreads == 256), "lane roles of the D = 512 scales");
 };
 
 // Raw int4 words and the scale / bias (fp16 bits, or fp32 with F32) of
-// this thread's keys of one tile.
+// this thread's keys of one tile (with LANE_SB: one value of the wave's).
 template <int D, bool F32>
 struct PfRaw {
   using SB = typename std::conditional<F32, float, uint16_t>::type;
   uint32_t kw[PfGeom<D>::KPT], vw[PfGeom<D>::KPT];
-  SB ks[PfGeom<D>::KPT], kb[PfGeom<D>::KPT], vs[PfGeom<D>::KPT], vb[PfGeom<D>::KPT];
+  SB ks[PfGeom<D>::NS], kb[PfGeom<D>::NS], vs[PfGeom<D>::NS], vb[PfGeom<D>::NS];
 };
+
+// The 32-bit value v of lane src of the wave.
+__device__ __forceinline__ uint32_t pf_from_lane(uint32_t v, int src) {
+  return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src << 2, static_cast<int>(v)));
+}
 
 // The key (0 .. 31 within the tile) held by V^T slot s.
 __device__ __forceinline__ int pf_vkey(int s) { return 16 * ((s >> 2) & 1) + 4 * (s >> 3) + (s & 3); }
@@ -112,10 +124,47 @@ __device__ __forceinline__ void pf_dequant(const PfRaw<D, F32>& raw, _Float16* k
   using Gm = PfGeom<D>;
   constexpr int KSTR = Gm::KSTR, VSTR = Gm::VSTR, KPT = Gm::KPT;
   typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+  // scale and bias of this thread's K keys and V slots
+  float kS[KPT], kB[KPT], vS[KPT], vB[KPT];
+  if constexpr (Gm::LANE_SB) {
+    // lane s holds K key kb0 + s / 8 of group s % 8, and V key s % 32 of
+    // group wv / 8 (lanes 0-31 and 32-63 hold the wave's two V groups)
+    const int lane = threadIdx.x & 63;
+    uint32_t kp = 0, vp = 0;
+    if constexpr (!F32) {
+      kp = static_cast<uint32_t>(raw.ks[0]) | (static_cast<uint32_t>(raw.kb[0]) << 16);
+      vp = static_cast<uint32_t>(raw.vs[0]) | (static_cast<uint32_t>(raw.vb[0]) << 16);
+    }
+#pragma unroll
+    for (int e = 0; e < KPT; ++e) {
+      const int sk = (e << 3) | (lane >> 3);
+      const int sv = (lane & 32) | (4 * (lane & 3) + (e & 3) + 16 * (e >> 2));
+      if constexpr (F32) {
+        kS[e] = __uint_as_float(pf_from_lane(__float_as_uint(raw.ks[0]), sk));
+        kB[e] = __uint_as_float(pf_from_lane(__float_as_uint(raw.kb[0]), sk));
+        vS[e] = __uint_as_float(pf_from_lane(__float_as_uint(raw.vs[0]), sv));
+        vB[e] = __uint_as_float(pf_from_lane(__float_as_uint(raw.vb[0]), sv));
+      } else {
+        const uint32_t kx = pf_from_lane(kp, sk), vx = pf_from_lane(vp, sv);
+        kS[e] = h2f(static_cast<uint16_t>(kx & 0xFFFFu));
+        kB[e] = h2f(static_cast<uint16_t>(kx >> 16));
+        vS[e] = h2f(static_cast<uint16_t>(vx & 0xFFFFu));
+        vB[e] = h2f(static_cast<uint16_t>(vx >> 16));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < KPT; ++e) {
+      kS[e] = sbf(raw.ks[e]);
+      kB[e] = sbf(raw.kb[e]);
+      vS[e] = sbf(raw.vs[e]);
+      vB[e] = sbf(raw.vb[e]);
+    }
+  }
 #pragma unroll
   for (int e = 0; e < KPT; ++e) {
     const int key = kb0 + e;
-    const float ks = sbf(raw.ks[e]), kbias = sbf(raw.kb[e]);
+    const float ks = kS[e], kbias = kB[e];
     float n[8];
     pf_nibbles(raw.kw[e], n);
     u32x4 kh, kl;
@@ -141,8 +190,8 @@ __device__ __forceinline__ void pf_dequant(const PfRaw<D, F32>& raw, _Float16* k
     vkpt vh, vl;
 #pragma unroll
     for (int e = 0; e < KPT; e += 2) {
-      const float x0 = fmaf(sbf(raw.vs[e]), nv[e][j], sbf(raw.vb[e]));
-      const float x1 = fmaf(sbf(raw.vs[e + 1]), nv[e + 1][j], sbf(raw.vb[e + 1]));
+      const float x0 = fmaf(vS[e], nv[e][j], vB[e]);
+      const float x1 = fmaf(vS[e + 1], nv[e + 1][j], vB[e + 1]);
       const v2bf_t h = v2bf_t{static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
       const uint32_t hb = __builtin_bit_cast(uint32_t, h);
       const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xFFFF0000u);
@@ -162,6 +211,10 @@ __device__ __forceinline__ void pf_load(PfRaw<D, F32>& R, const SdpaParams& p, i
                                         int last, int wk, int kk0, int wv, int kv0) {
   using Gm = PfGeom<D>;
   using SB = typename PfRaw<D, F32>::SB;
+  const SB* ks = static_cast<const SB*>(p.ks);
+  const SB* kb = static_cast<const SB*>(p.kb);
+  const SB* vs = static_cast<const SB*>(p.vs);
+  const SB* vb = static_cast<const SB*>(p.vb);
 #pragma unroll
   for (int e = 0; e < Gm::KPT; ++e) {
     const int64_t rk = row0 + min(t0 + kk0 + e, last);
@@ -169,15 +222,30 @@ __device__ __forceinline__ void pf_load(PfRaw<D, F32>& R, const SdpaParams& p, i
     const int64_t rv = row0 + min(t0 + pf_vkey(kv0) + (e & 3) + 16 * (e >> 2), last);
     R.kw[e] = __builtin_nontemporal_load(p.kq + rk * Gm::W + wk);
     R.vw[e] = __builtin_nontemporal_load(p.vq + rv * Gm::W + wv);
-    R.ks[e] = static_cast<const SB*>(p.ks)[rk * (D / 64) + (wk >> 3)];
-    R.kb[e] = static_cast<const SB*>(p.kb)[rk * (D / 64) + (wk >> 3)];
-    R.vs[e] = static_cast<const SB*>(p.vs)[rv * (D / 64) + (wv >> 3)];
-    R.vb[e] = static_cast<const SB*>(p.vb)[rv * (D / 64) + (wv >> 3)];
+    if constexpr (!Gm::LANE_SB) {
+      R.ks[e] = ks[rk * (D / 64) + (wk >> 3)];
+      R.kb[e] = kb[rk * (D / 64) + (wk >> 3)];
+      R.vs[e] = vs[rv * (D / 64) + (wv >> 3)];
+      R.vb[e] = vb[rv * (D / 64) + (wv >> 3)];
+    }
+  }
+  if constexpr (Gm::LANE_SB) {
+    // K key kk0 + lane / 8 (the wave's keys) of group lane % 8; V key
+    // lane % 32 of group wv / 8
+    const int lane = threadIdx.x & 63;
+    const int64_t rk = row0 + min(t0 + kk0 + (lane >> 3), last);
+    const int64_t rv = row0 + min(t0 + (lane & 31), last);
+    R.ks[0] = ks[rk * (D / 64) + (lane & 7)];
+    R.kb[0] = kb[rk * (D / 64) + (lane & 7)];
+    R.vs[0] = vs[rv * (D / 64) + (wv >> 3)];
+    R.vb[0] = vb[rv * (D / 64) + (wv >> 3)];
   }
 }
 
 // D = 512: one wave per SIMD (q hi / lo and the O^T accumulators take 256
-// registers), 145 KB of LDS
+// registers), 145 KB of LDS.  With one wave per SIMD nothing hides LDS
+// latency: the products' operands are read four k-steps / blocks ahead,
+// which the scale / bias lane sharing (LANE_SB) leaves registers for.
 template <int D, bool F32>
 __global__ __launch_bounds__(kPfThreads)
 __attribute__((amdgpu_waves_per_eu(D == 512 ? 1 : 2, D == 512 ? 1 : 2)))
@@ -188,7 +256,7 @@ void prefill_int4_kernel(SdpaParams p) {
   constexpr int KPT = Gm::KPT;
   __shared__ __attribute__((aligned(16))) _Float16 khi[kPfKeys * KSTR], klo[kPfKeys * KSTR];
   __shared__ __attribute__((aligned(16))) __bf16 vthi[D * VSTR], vtlo[D * VSTR];
-  static_assert(DB % 4 == 0, "V^T reads are issued four blocks ahead");
+  static_assert(CH % 4 == 0 && DB % 4 == 0, "reads are issued four k-steps / blocks ahead");
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, c = lane >> 4;
@@ -271,14 +339,23 @@ void prefill_int4_kernel(SdpaParams p) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      // K reads of four k-steps issued ahead of their products
 #pragma unroll
-      for (int ch = 0; ch < CH; ++ch) {
-        const int off = (16 * half + m) * KSTR + 32 * ch + 8 * c;
-        const v8h ah = *reinterpret_cast<const v8h*>(&khi[off]);
-        const v8h al = *reinterpret_cast<const v8h*>(&klo[off]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[ch], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ch], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[ch], acc, 0, 0, 0);
+      for (int c0 = 0; c0 < CH; c0 += 4) {
+        v8h ah[4], al[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int off = (16 * half + m) * KSTR + 32 * (c0 + j) + 8 * c;
+          ah[j] = *reinterpret_cast<const v8h*>(&khi[off]);
+          al[j] = *reinterpret_cast<const v8h*>(&klo[off]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], qh[c0 + j], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], ql[c0 + j], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], qh[c0 + j], acc, 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
