@@ -443,7 +443,7 @@ void prefill_int4_kernel(SdpaParams p) {
 // while compute waves 4-7 run tile st from the other; one barrier per step.
 // Both roles pass the same number of barriers (an even number of steps;
 // a step past the last tile dequantizes clamped rows, whose scores the
-// mask drops).  Two slots take 141 KB at D = 256, so D = 512 keeps the
+// mask drops).  Two slots take 146 KB at D = 256, so D = 512 keeps the
 // kernel above.
 template <int D, bool F32>
 __global__ __launch_bounds__(2 * kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
