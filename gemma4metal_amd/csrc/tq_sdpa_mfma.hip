@@ -530,21 +530,34 @@ void sdpa_int4_mfma_kernel(SdpaParams p) {
     constexpr int NU = PACK ? 1 : 2;
     float sc[4 * NU];
     auto kq_tile = [&](int tile, v4i (&acc)[3], int img) {
+      // B operands live in LDS (16 B per lane per MFMA) to keep the wave
+      // within 256 registers; those of half the tile's k-steps are read
+      // ahead of their products (the compiler otherwise keeps two reads in
+      // flight)
+      constexpr int RS = KM >= 2 ? KM / 2 : 1;
 #pragma unroll
-      for (int i = 0; i < KM; ++i) {
-        const uint32_t w0 = B.kw[tile][2 * i], w1 = B.kw[tile][2 * i + 1];
-        const v4i a = v4i{static_cast<int>(w0 & 0x0F0F0F0Fu),
-                          static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
-                          static_cast<int>(w1 & 0x0F0F0F0Fu),
-                          static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+      for (int i0 = 0; i0 < KM; i0 += RS) {
+        uint4 bu[RS][3];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          // B operands live in LDS (16 B per lane per MFMA) to keep the wave
-          // within 256 registers
-          const uint4 u = bq_addr[img][(k * KM + i) * QCOL * QCC];
-          const v4i bq = v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z),
-                             static_cast<int>(u.w)};
-          acc[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, acc[k], 0, 0, 0);
+        for (int ii = 0; ii < RS; ++ii)
+#pragma unroll
+          for (int k = 0; k < 3; ++k) bu[ii][k] = bq_addr[img][(k * KM + i0 + ii) * QCOL * QCC];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ii = 0; ii < RS; ++ii) {
+          const int i = i0 + ii;
+          const uint32_t w0 = B.kw[tile][2 * i], w1 = B.kw[tile][2 * i + 1];
+          const v4i a = v4i{static_cast<int>(w0 & 0x0F0F0F0Fu),
+                            static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
+                            static_cast<int>(w1 & 0x0F0F0F0Fu),
+                            static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+          for (int k = 0; k < 3; ++k) {
+            const uint4 u = bu[ii][k];
+            const v4i bq = v4i{static_cast<int>(u.x), static_cast<int>(u.y), static_cast<int>(u.z),
+                               static_cast<int>(u.w)};
+            acc[k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bq, acc[k], 0, 0, 0);
+          }
         }
       }
     };
