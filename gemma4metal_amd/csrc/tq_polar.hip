@@ -1744,6 +1744,7 @@ int polar_sdpa_params(SdpaParams& p, int Hq, int Hkv, int D, int n, int cap, flo
   p.max_splits = max_splits;
   p.denom_eps = denom_eps;
   grid = dim3(max_splits, Hkv * n_sub, 1);
+  p.cnt_stride = counter_stride(Hq);
   return TQ_OK;
 }
 

@@ -568,6 +568,7 @@ int sdpa_common(const void* q, int q_dtype, const uint32_t* kq, const void* ks, 
   p.cus = target_wgs();
 
   dim3 grid(max_splits, Hkv * n_sub, (batch + pq - 1) / pq);
+  p.cnt_stride = counter_stride(static_cast<int64_t>(grid.z) * Hq);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (pl.kernel) {
     case SdpaKernel::prefill_tiles:

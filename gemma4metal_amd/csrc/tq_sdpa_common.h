@@ -7,6 +7,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 // The split-K completion protocol below (Finalize::run: relaxed agent-scope
 // partial stores and loads, one relaxed counter atomic, no L2 write-back or
 // invalidate) is correct because of how gfx950 executes those instructions:
@@ -70,7 +72,18 @@ struct SdpaParams {
   // from the longest-first order of ragged_job.  cus: compute units.
   int lpt;
   int cus;
+  // ints between the split counters of consecutive (sequence, head) rows
+  // (counter_stride of the launch's counter count, set on the host)
+  int cnt_stride;
 };
+
+// Counter `c` of a launch with n counters in use sits at ws_cnt[c * stride]:
+// up to 32 ints (one 128 B line) from its neighbours, as far as the counter
+// region allows -- the atomics of every head's last splits arrive together
+// at the end of a launch, and on one shared line they serialise.
+inline int counter_stride(int64_t n) {
+  return static_cast<int>(std::min<int64_t>(32, kMaxCounters / std::max<int64_t>(n, 1)));
+}
 
 // Kernel arguments arrive through scalar loads from the kernarg segment, one
 // memory round trip per batch of loads.  Left to itself, the compiler places
@@ -83,7 +96,7 @@ __device__ __forceinline__ void pin_args(const SdpaParams& p) {
   asm volatile("" ::"s"(p.q), "s"(p.kq), "s"(p.ks), "s"(p.kb), "s"(p.vq), "s"(p.vs), "s"(p.vb),
                "s"(p.seq_lens), "s"(p.windows), "s"(p.q_dtype), "s"(p.Hq), "s"(p.Hkv), "s"(p.cap),
                "s"(p.gqa), "s"(p.n_sub), "s"(p.n), "s"(p.window), "s"(p.n_clamp),
-               "s"(p.scale_log2), "s"(p.chunk), "s"(p.prefill));
+               "s"(p.scale_log2), "s"(p.chunk), "s"(p.prefill), "s"(p.ws_cnt), "s"(p.cnt_stride));
 }
 
 // Batch index of the cache that batch element b reads.
@@ -473,13 +486,10 @@ struct Finalize {
     __syncthreads();
     __shared__ int s_last;
     if (threadIdx.x == 0) {
-      // Counter `counter` (< gridDim.z * Hq, checked on the host) sits up to
-      // 32 ints (one 128 B line) from its neighbours, as far as the region
-      // allows: the atomics of every head's last splits arrive together at
-      // the end of a launch, and on one shared line they serialise.
-      const int64_t ncnt = static_cast<int64_t>(gridDim.z) * p.Hq;
-      const int stride = static_cast<int>(min(int64_t{32}, kMaxCounters / ncnt));
-      int* cnt = p.ws_cnt + static_cast<int64_t>(counter) * stride;
+      // counter `counter` < gridDim.z * Hq (checked on the host); its
+      // spacing comes with the arguments, so nothing but the atomic lies
+      // between the barrier and the counter's value
+      int* cnt = p.ws_cnt + static_cast<int64_t>(counter) * p.cnt_stride;
       const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = (old == S - 1);
       // leave the workspace zeroed for the next call -- with an atomic RMW,
