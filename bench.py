@@ -163,11 +163,12 @@ GRAPH_LAUNCHES = 32
 
 
 def time_graph(torch, fn, n, steps, warmup):
-    """time_launches for launches shorter than the host's issue time: fn(0)
-    .. fn(n - 1) are captured in one HIP graph (on a stream warmed up
-    eagerly first, so nothing is allocated during capture), and the replays
-    are timed; returns the same (ms per launch, mean, median) triple, per
-    launch."""
+    """time_launches of launches replayed from a graph, the way a captured
+    decode step runs them (and the only way to time launches shorter than
+    the host's ~10 us issue time): fn(0) .. fn(n - 1) are captured in one HIP
+    graph (on a stream warmed up eagerly first, so nothing is allocated
+    during capture), and the replays are timed; returns the same (ms per
+    launch, mean, median) triple, per launch."""
     cs = torch.cuda.Stream()
     with torch.cuda.stream(cs):
         for i in range(n):
@@ -180,6 +181,17 @@ def time_graph(torch, fn, n, steps, warmup):
     reps = max(1, steps // n)
     ms, mean, med = time_launches(torch, lambda i: g.replay(), reps, max(1, warmup // n))
     return ms / n, mean / n, med / n
+
+
+def time_graph_and_direct(torch, fn, nsets, steps, warmup):
+    """(ms per step as HIP-graph replays, ms per step issued directly, graph
+    launches): fn's steps timed as replays of one graph of
+    max(GRAPH_LAUNCHES, nsets) steps over the rotated sets, and as direct
+    back-to-back calls."""
+    ng = max(GRAPH_LAUNCHES, nsets)
+    ms_graph = time_graph(torch, fn, ng, steps, warmup)[0]
+    ms_direct = time_launches(torch, fn, steps, warmup)[0]
+    return ms_graph, ms_direct, ng
 
 
 def cpu_baseline(args, cache_host, q_host, Hq, Hkv, D, L, W, nbytes):
@@ -350,13 +362,17 @@ def main():
         out = torch.empty((Hg, Dg), dtype=torch.float32, device="cuda")
         nbytes = O.decode_bytes(Hg, Hkvg, Dg, L, sb_bytes=sb_bytes)
         plan = tq.sdpa_plan(Hg, Hkvg, Dg, L, sb_dtype=sbt)
-        ms_step, _, _ = time_launches(torch, lambda i: tq.sdpa_int4(
-            qs[i % nsets], *sets[i % nsets], Hg // Hkvg, 1.0, 0, out=out), args.steps, args.warmup)
+        ms_step, ms_direct, ng = time_graph_and_direct(torch, lambda i: tq.sdpa_int4(
+            qs[i % nsets], *sets[i % nsets], Hg // Hkvg, 1.0, 0, out=out), nsets, args.steps,
+            args.warmup)
         gbs = nbytes / (ms_step * 1e-3) / 1e9
         emit({"metric": "int4-KV decode SDPA GB/s, Gemma global layer (D 512, GQA 8)",
               "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
               "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
               "us_per_layer": round(ms_step * 1e3, 2), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+              "timing": f"HIP graph of {ng} layers (attention + merge launches) over the "
+                        f"{nsets} sets, replayed",
+              "us_per_layer_direct_launches": round(ms_direct * 1e3, 2),
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
               "dtype": precision_note(args.sb),
               "data": (f"synthetic; {nsets} rotated KV sets "
@@ -600,11 +616,11 @@ def bench_polar(args, torch, gen):
         s = i % nsets
         codec.score_q(qs_[s], *sets[s][0])
 
-    ms_step, _, _ = time_launches(torch, step, args.steps, args.warmup)
-    ms_two, _, _ = time_launches(torch, two_launch, args.steps, args.warmup)
-    ms_attn, _, _ = time_launches(torch, attn_only, args.steps, args.warmup)
-    ms_score, _, _ = time_launches(torch, score_only, args.steps, args.warmup)
-    ms_score_q, _, _ = time_launches(torch, score_q, args.steps, args.warmup)
+    ms_step, ms_step_direct, ng = time_graph_and_direct(torch, step, nsets, args.steps, args.warmup)
+    ms_two = time_graph_and_direct(torch, two_launch, nsets, args.steps, args.warmup)[0]
+    ms_attn = time_graph_and_direct(torch, attn_only, nsets, args.steps, args.warmup)[0]
+    ms_score = time_graph_and_direct(torch, score_only, nsets, args.steps, args.warmup)[0]
+    ms_score_q = time_graph_and_direct(torch, score_q, nsets, args.steps, args.warmup)[0]
     score_bytes = Hkv * L * 68 + 2 * Hq * D * 4 + Hq * L * 4
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     gbs_attn = nbytes / (ms_attn * 1e-3) / 1e9
@@ -612,6 +628,9 @@ def bench_polar(args, torch, gen):
           "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
           "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
           "us_per_layer": round(ms_step * 1e3, 2), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+          "timing": f"HIP graph of {ng} steps over the {nsets} sets, replayed (every form below "
+                    "too)",
+          "us_per_layer_direct_launches": round(ms_step_direct * 1e3, 2),
           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
           "dtype": "polar7 angles + 128-bit QJL sketch (fp16 norms), int4 V (fp16 scale/bias), "
                    "f32 q, f32 accumulate",
